@@ -1,0 +1,190 @@
+"""Headline benchmark: FP8 paged decode attention, BASELINE config 3, on one MI355X.
+
+A step is one decode step's attention over all 28 layers of Qwen3-0.6B: 256 sequences (one
+query token each), contexts U{100..1024} + U{0..1024}, 16 query / 8 kv heads, head_dim 128,
+FP8 e4m3 cache in 256-token blocks with per-(token, head) scales (the reference's scale mode),
+seeded random block tables. Each layer has its own cache (28 distinct ~630 MB K+V pools), so
+every layer's KV read is cold in the 256 MB last-level cache, as in a real decode step.
+
+`value` is algorithmic KV-read bandwidth in GB/s: sum over layers of
+  sum_t kv_len(t) * KV * (2*HD + 8)  +  2 * T * H * HD * 2   bytes
+divided by the timed wall time of K steps (inputs resident in HBM before timing starts).
+
+Prints one JSON line (rank 0). Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "FP8 paged-decode KV-read GB/s (% of HBM peak), 256 seqs; e2e output tok/s"
+HBM_PEAK_GBS = 8000.0
+LAYERS = 28
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config3_traffic.txt"
+
+
+def read_traffic():
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 PMC summary."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(b, reps: int = 5):
+    """The oracle (scalar C restatement, OpenMP over (token, kv head)) on one full layer of the
+    same workload, timed on this host: median of `reps` after one warm-up."""
+    import numpy as np
+
+    import oracle
+    from cppvllm_amd import workloads
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    oracle.set_threads(threads)
+
+    def host(t):
+        import torch
+        if t.dtype == torch.bfloat16:
+            return t.cpu().view(torch.int16).numpy().view(np.uint16)
+        return t.cpu().numpy()
+
+    args = [host(b[k]) for k in ("q", "k_cache", "v_cache", "k_scale", "v_scale", "block_tables", "token_seq",
+                                 "token_kv_len")]
+    H, KV, HD, BS = b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
+    times = []
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        oracle.paged_attention_fp8(*args, H, KV, HD, BS, oracle.PER_TOKEN_HEAD, b["scale"])
+        if i:
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    nbytes = workloads.attention_bytes(args[7].tolist())
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"one layer of config 3 (all 256 tokens, {nbytes / 1e6:.1f} MB algorithmic), "
+                      f"median of {reps} after 1 warm-up: {med * 1e3:.1f} ms/layer"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--split-tokens", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(decode attention shards by sequence or kv head with no exchange; see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from cppvllm_amd import _lib, workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    print("bench: building config 3 on device", flush=True, file=sys.stderr)
+    b = workloads.config3(device=dev)
+    lens = b["token_kv_len"].cpu().tolist()
+    T, H, KV, HD, BS = len(lens), b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
+    W = b["block_tables"].shape[1]
+    layers = []
+    for l in range(args.layers):
+        if l == 0:
+            layers.append((b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"]))
+        else:
+            layers.append(tuple(x.clone() for x in (b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"])))
+    lib = _lib.lib()
+    ws_bytes = lib.cvh_paged_attention_workspace_bytes(T, H, KV, HD, W, BS, args.split_tokens)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(b["q"])
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    fixed = (out.data_ptr(), b["q"].data_ptr())
+    tail = (b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(), b["token_kv_len"].data_ptr(), T, H, KV, HD,
+            BS, _lib.SCALE_PER_TOKEN_HEAD, b["scale"], args.split_tokens, ws.data_ptr(), ws_bytes, sp)
+    layer_ptrs = [tuple(x.data_ptr() for x in lay) for lay in layers]
+    fn = lib.cvh_paged_attention_fp8_ex
+
+    def step():
+        for lp in layer_ptrs:
+            code = fn(*fixed, *lp, *tail)
+            if code:
+                raise _lib.CvhError("paged_attention_fp8", code)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # per-layer events over the timed region, on the stream the kernels are launched on
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps * len(layer_ptrs))]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    i = 0
+    for _ in range(args.steps):
+        for lp in layer_ptrs:
+            evs[i][0].record(stream)
+            code = fn(*fixed, *lp, *tail)
+            evs[i][1].record(stream)
+            i += 1
+            if code:
+                raise _lib.CvhError("paged_attention_fp8", code)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    layer_ms = [a.elapsed_time(z) for a, z in evs]
+    avg_layer_ms = sum(layer_ms) / len(layer_ms)
+
+    bytes_layer = workloads.attention_bytes(lens)
+    bytes_step = bytes_layer * len(layer_ptrs)
+    value = bytes_step * args.steps / (total_ms / 1e3) / 1e9
+    achieved = bytes_layer / (avg_layer_ms / 1e3) / 1e9
+    traffic = read_traffic()
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) K/V quantised to e4m3 per (token, head); random block tables)",
+        "config": {
+            "workload": "BASELINE config 3: 256-seq FP8 paged decode step, 28 layers, distinct per-layer caches",
+            "seqs": T, "ctx_sum": int(sum(lens)), "ctx_min": int(min(lens)), "ctx_max": int(max(lens)),
+            "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "block_size": BS, "layers": len(layer_ptrs),
+            "scale_mode": "per_token_head", "split_tokens": lib.cvh_paged_attention_split_tokens(T, KV, W, BS)
+            if args.split_tokens == 0 else args.split_tokens,
+            "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        },
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "paged attention op per layer (decode kernel + split merge)",
+                     "avg_launch_us": round(avg_layer_ms * 1e3, 2)},
+    }
+    if not args.no_cpu:
+        print("bench: CPU baseline (oracle, one layer)", flush=True, file=sys.stderr)
+        res["cpu_baseline"] = cpu_baseline(b)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,86 @@
+"""ctypes binding of the C ABI in ``include/cppvllm_hip.h`` (library ``libcppvllm_hip.so``).
+
+The library is the product: there is no fallback. ``lib()`` raises if the shared object is
+missing or does not export a declared symbol.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libcppvllm_hip.so"
+HEADER = PKG.parent / "include" / "cppvllm_hip.h"
+
+CVH_OK = 0
+CVH_ERR_INVALID_ARG = 1
+CVH_ERR_UNSUPPORTED = 2
+CVH_ERR_WORKSPACE = 3
+CVH_ERR_LAUNCH = 4
+ERROR_NAMES = {0: "CVH_OK", 1: "CVH_ERR_INVALID_ARG", 2: "CVH_ERR_UNSUPPORTED", 3: "CVH_ERR_WORKSPACE",
+               4: "CVH_ERR_LAUNCH"}
+
+SCALE_PER_TOKEN_HEAD = 0
+SCALE_PER_TENSOR = 1
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
+
+vp, i64, i32, f64, f32, sz = C.c_void_p, C.c_int64, C.c_int, C.c_double, C.c_float, C.c_size_t
+
+# name -> (restype, argtypes), in the order of include/cppvllm_hip.h
+SIGNATURES = {
+    "cvh_paged_attention_fp8": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32, f64,
+                                      vp, sz, vp]),
+    "cvh_paged_attention_fp8_ex": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32, f64,
+                                         i32, vp, sz, vp]),
+    "cvh_paged_attention_workspace_bytes": (sz, [i64, i32, i32, i32, i64, i32, i32]),
+    "cvh_paged_attention_split_tokens": (i32, [i64, i32, i64, i32]),
+    "cvh_rms_norm": (i32, [vp, vp, vp, i64, i32, f64, i32, vp]),
+    "cvh_add_rms_norm": (i32, [vp, vp, vp, vp, i64, i32, f64, i32, vp]),
+    "cvh_qk_norm_rope_kv_write_fp8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i32, i32,
+                                            i32, i32, i32, f64, vp]),
+    "cvh_build_token_metadata": (i32, [vp, i64, vp, i64, vp, i64, i32, vp, vp, vp, vp]),
+    "cvh_rope_tables_host": (i32, [vp, vp, i64, i32, f64]),
+    "cvh_fp8_e4m3_quantize": (i32, [vp, vp, i64, f32, vp]),
+    "cvh_version": (C.c_char_p, []),
+}
+
+_LIB = None
+
+
+class CvhError(RuntimeError):
+    """A non-zero status returned across the C ABI."""
+
+    def __init__(self, fn: str, code: int):
+        super().__init__(f"{fn} failed: {ERROR_NAMES.get(code, code)}")
+        self.code = code
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/cppvllm_hip.h."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(cvh_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib() -> C.CDLL:
+    """Load libcppvllm_hip.so (built by cppvllm_amd.build). Raises if it is missing."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = Path(os.environ.get("CVH_LIB", LIB_PATH))
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: build it with `python -m cppvllm_amd.build` "
+                           "(the HIP library is required; there is no fallback path)")
+    handle = C.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = handle
+    return handle
+
+
+def check(fn: str, code: int) -> None:
+    if code != CVH_OK:
+        raise CvhError(fn, code)

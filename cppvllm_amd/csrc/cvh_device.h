@@ -1,0 +1,105 @@
+// Device helpers shared by the gfx950 kernels: bf16/f16 rounding, OCP e4m3 encode/decode and
+// wavefront reductions. Every rounding helper here has a bit-identical host restatement in the
+// CPU oracle (oracle/cvh_oracle.c), which is what makes the cache bytes bit-exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/cppvllm_hip.h"
+
+namespace cvh {
+
+// ---- bf16 ------------------------------------------------------------------------------------
+// float -> bf16 bits, round to nearest even; NaN -> quiet NaN with the sign kept.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ---- fp16 (IEEE half), only used by the f16 instantiation of the norm kernels ----------------
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    const _Float16 h = static_cast<_Float16>(f);     // v_cvt_f16_f32: round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+// Storage-type traits for the norm kernels (bf16 / f16 / f32 rows).
+template <int DT> struct Elem;
+template <> struct Elem<CVH_DTYPE_BF16> {
+    using T = uint16_t;
+    static __device__ __forceinline__ float load(T v) { return bf16_bits_to_f32(v); }
+    static __device__ __forceinline__ T store(float f) { return f32_to_bf16_bits(f); }
+};
+template <> struct Elem<CVH_DTYPE_F16> {
+    using T = uint16_t;
+    static __device__ __forceinline__ float load(T v) { return f16_bits_to_f32(v); }
+    static __device__ __forceinline__ T store(float f) { return f32_to_f16_bits(f); }
+};
+template <> struct Elem<CVH_DTYPE_F32> {
+    using T = float;
+    static __device__ __forceinline__ float load(T v) { return v; }
+    static __device__ __forceinline__ T store(float f) { return f; }
+};
+
+// ---- OCP e4m3fn ------------------------------------------------------------------------------
+// Encode with round-to-nearest-even and saturation to +-448 (the __NV_SATFINITE behaviour of the
+// reference, kernels/fused_ops.cu:42-44). NaN -> 0x7F. Written with integer ops so the exact same
+// bytes come out of the host restatement; derived from the OCP 8-bit FP spec (bias 7, 3 mantissa
+// bits, max normal 448 = 0x7E, subnormals k*2^-9).
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7fu;                       // NaN
+    if (a >= 0x43e00000u) return sign | 0x7eu;               // |x| >= 448 (incl. inf): saturate
+    if (a < 0x3c800000u) {                                   // |x| < 2^-6: subnormal grid k*2^-9
+        const float k = __builtin_rintf(__uint_as_float(a) * 512.0f);   // exact scale, RNE
+        return sign | static_cast<uint32_t>(k);              // k == 8 is the smallest normal 0x08
+    }
+    const uint32_t e = (a >> 23) - 127u + 7u;                // 1..15
+    uint32_t code = (e << 3) | ((a >> 20) & 7u);
+    const uint32_t rem = a & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (code & 1u))) ++code;
+    if (code > 0x7eu) code = 0x7eu;
+    return sign | code;
+}
+
+// Hardware OCP e4m3 -> f32 of the four codes of w (byte i -> f[i]).
+// gfx950's v_cvt_pk_f32_fp8 is OCP e4m3fn and exact for every finite code.
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+    f[0] = lo[0];
+    f[1] = lo[1];
+    f[2] = hi[0];
+    f[3] = hi[1];
+}
+
+// ---- DPP helpers (within rows of 16 lanes) ---------------------------------------------------
+// Sum with the lane at (lane ^ 1), (lane ^ 2) inside a quad: quad_perm patterns.
+__device__ __forceinline__ float dpp_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+// row_half_mirror: lane i <-> 7-i inside each group of 8. After the xor1/xor2 levels a quad is
+// uniform, so this pairs quad 0 with quad 1 exactly like an xor-4 exchange would.
+__device__ __forceinline__ float dpp_half_mirror(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+}
+// row_mirror: lane i <-> 15-i inside each row of 16 (an xor-8 exchange once halves are uniform).
+__device__ __forceinline__ float dpp_mirror(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+}  // namespace cvh

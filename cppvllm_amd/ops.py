@@ -1,0 +1,146 @@
+"""Torch-tensor mirror of cppvllm's kernel-layer API, backed by the gfx950 C ABI.
+
+Names, argument order and meaning follow the reference's free functions:
+  * ``paged_attention_fp8``            — kernels/paged_attention.h:5-7
+  * ``fused.rms_norm`` / ``add_rms_norm`` / ``qk_norm_rope_kv_write_fp8`` — kernels/fused_ops.h:7-15
+Shapes that the reference reads from tensor metadata are read the same way here
+(``q.size(1)`` = heads, ``k_cache.size(1)`` = block size, ``k_cache.size(2)`` = kv heads,
+``block_tables.size(1)`` = table width; kernels/paged_attention.cu:398-400,432,463-464).
+Errors the reference raises with TORCH_CHECK raise ``CvhError``/``ValueError`` here.
+
+Every call goes to the HIP library on torch's current stream. There is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+import types
+
+import torch
+
+from . import _lib
+from ._lib import SCALE_PER_TENSOR, SCALE_PER_TOKEN_HEAD, check
+
+_DT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None or (isinstance(t, torch.Tensor) and t.numel() == 0) else t.data_ptr()
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("cppvllm_amd ops take device tensors only")
+        if t is not None and not t.is_contiguous():
+            raise ValueError("cppvllm_amd ops take contiguous tensors only")
+
+
+def _scale_mode(k_scale: torch.Tensor) -> int:
+    return SCALE_PER_TENSOR if k_scale.numel() == 1 else SCALE_PER_TOKEN_HEAD
+
+
+def paged_attention_workspace(num_tokens: int, n_heads: int, n_kv_heads: int, head_dim: int, table_width: int,
+                              block_size: int, split_tokens: int = 0, device="cuda") -> torch.Tensor:
+    """Preallocated split-K workspace (what the reference allocates per call, paged_attention.cu:415-421)."""
+    n = _lib.lib().cvh_paged_attention_workspace_bytes(num_tokens, n_heads, n_kv_heads, head_dim, table_width,
+                                                      block_size, split_tokens)
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
+
+
+def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len,
+                        scale: float, *, workspace: torch.Tensor | None = None, split_tokens: int = 0) -> None:
+    """FP8 paged attention over a ragged batch of query tokens (kernels/paged_attention.cu:459-473).
+
+    out, q: bf16 [T, H, HD]; k_cache, v_cache: uint8 [NB, BS, KV, HD]; k_scale, v_scale: float32
+    [NB, BS, KV] (memory order [NB][KV][BS]) or one element each (per-tensor); block_tables int64
+    [S, W]; token_seq, token_kv_len int64 [T].
+    """
+    T = q.size(0)
+    if T == 0:
+        return
+    _require_cuda(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len)
+    H, HD = q.size(1), q.size(2)
+    BS, KV = k_cache.size(1), k_cache.size(2)
+    W = block_tables.size(1)
+    if workspace is None:
+        workspace = paged_attention_workspace(T, H, KV, HD, W, BS, split_tokens, q.device)
+    code = _lib.lib().cvh_paged_attention_fp8_ex(
+        out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
+        v_scale.data_ptr(), block_tables.data_ptr(), W, token_seq.data_ptr(), token_kv_len.data_ptr(), T, H, KV,
+        HD, BS, _scale_mode(k_scale), float(scale), int(split_tokens), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(q))
+    check("paged_attention_fp8", code)
+
+
+def _rms_norm(out, x, w, eps):
+    if x.size(0) == 0:
+        return
+    _require_cuda(out, x, w)
+    code = _lib.lib().cvh_rms_norm(out.data_ptr(), x.data_ptr(), w.data_ptr(), x.size(0), x.size(1), float(eps),
+                                   _DT[x.dtype], _stream(x))
+    check("rms_norm", code)
+
+
+def _add_rms_norm(resid, x, w, out, eps):
+    if resid.size(0) == 0:
+        return
+    _require_cuda(resid, x, w, out)
+    code = _lib.lib().cvh_add_rms_norm(resid.data_ptr(), x.data_ptr(), w.data_ptr(), out.data_ptr(), resid.size(0),
+                                       resid.size(1), float(eps), _DT[resid.dtype], _stream(resid))
+    check("add_rms_norm", code)
+
+
+def _qk_norm_rope_kv_write_fp8(q_out, qkv, q_norm, k_norm, cos, sin, positions, slots, k_cache, v_cache, k_scale,
+                               v_scale, k_dense, v_dense, n_heads: int, n_kv_heads: int, eps: float) -> None:
+    T, HD = q_out.size(0), q_out.size(2)
+    if T == 0:
+        return
+    _require_cuda(q_out, qkv, q_norm, k_norm, cos, sin, positions, slots, k_cache, v_cache, k_scale, v_scale)
+    BS = k_cache.size(1)
+    code = _lib.lib().cvh_qk_norm_rope_kv_write_fp8(
+        q_out.data_ptr(), qkv.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        positions.data_ptr(), slots.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
+        v_scale.data_ptr(), _ptr(k_dense), _ptr(v_dense), T, int(n_heads), int(n_kv_heads), HD, BS,
+        _scale_mode(k_scale), float(eps), _stream(q_out))
+    check("qk_norm_rope_kv_write_fp8", code)
+
+
+# The reference's `namespace fused` (kernels/fused_ops.h:5).
+fused = types.SimpleNamespace(rms_norm=_rms_norm, add_rms_norm=_add_rms_norm,
+                              qk_norm_rope_kv_write_fp8=_qk_norm_rope_kv_write_fp8)
+
+
+def build_token_metadata(cu_seqlens, positions, block_tables, block_size: int):
+    """(token_seq, slot_mapping, token_kv_len) for a ragged batch (model/model_architecture.cpp:137-147)."""
+    T = positions.size(0)
+    S = cu_seqlens.size(0) - 1
+    _require_cuda(cu_seqlens, positions, block_tables)
+    dev = positions.device
+    seq = torch.empty(T, dtype=torch.int64, device=dev)
+    slot = torch.empty(T, dtype=torch.int64, device=dev)
+    kvl = torch.empty(T, dtype=torch.int64, device=dev)
+    if T == 0:
+        return seq, slot, kvl
+    code = _lib.lib().cvh_build_token_metadata(cu_seqlens.data_ptr(), S, positions.data_ptr(), T,
+                                               block_tables.data_ptr(), block_tables.size(1), int(block_size),
+                                               seq.data_ptr(), slot.data_ptr(), kvl.data_ptr(), _stream(positions))
+    check("build_token_metadata", code)
+    return seq, slot, kvl
+
+
+def rope_tables(max_position: int, head_dim: int, theta: float):
+    """Host float32 cos/sin tables [max_position, head_dim/2] (model/model_architecture.cpp:67-75)."""
+    cos = torch.empty(max_position, head_dim // 2, dtype=torch.float32)
+    sin = torch.empty_like(cos)
+    check("rope_tables", _lib.lib().cvh_rope_tables_host(cos.data_ptr(), sin.data_ptr(), max_position, head_dim,
+                                                         float(theta)))
+    return cos, sin
+
+
+def fp8_e4m3_quantize(dst, src, inv_scale: float) -> None:
+    _require_cuda(dst, src)
+    check("fp8_e4m3_quantize", _lib.lib().cvh_fp8_e4m3_quantize(dst.data_ptr(), src.data_ptr(), src.numel(),
+                                                                 float(inv_scale), _stream(src)))

@@ -1,0 +1,157 @@
+/*
+ * cppvllm_hip.h — C ABI of the MI355X (gfx950) FP8 paged-decode hot path.
+ *
+ * Drop-in boundary for the kernel layer of cppvllm. Each entry point replaces one
+ * at::Tensor-taking free function of the reference kernel layer; tensors become plain
+ * device pointers plus the shapes the reference reads from tensor metadata, and the
+ * current c10 stream becomes an explicit hipStream_t. No libtorch types cross this ABI.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers unless stated otherwise; the caller owns every buffer.
+ *   - No entry point allocates device memory or synchronises the stream (capture-safe).
+ *   - Return value: CVH_OK (0) or a CVH_ERR_* code. Nothing throws across this ABI.
+ *   - num_tokens == 0 is a successful no-op (the reference returns early,
+ *     kernels/paged_attention.cu:462, kernels/fused_ops.cu:227,237,252).
+ *
+ * KV-cache layout (one layer), identical to the reference (engine/model_runner.cpp:104-113):
+ *   k_cache, v_cache : uint8 OCP e4m3fn, [num_blocks][block_size][n_kv_heads][head_dim]
+ *   k_scale, v_scale : float32,
+ *       CVH_SCALE_PER_TOKEN_HEAD: memory order [num_blocks][n_kv_heads][block_size]
+ *                                 (kernels/fused_ops.cu:136,185; paged_attention.cu:224)
+ *       CVH_SCALE_PER_TENSOR    : one float each (k_scale[0], v_scale[0]); read-only inputs.
+ *   slot s addresses token (s / block_size, s % block_size) of the pool.
+ */
+#ifndef CPPVLLM_HIP_H
+#define CPPVLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* cvh_stream_t; /* == hipStream_t; NULL = default stream */
+
+enum {
+    CVH_OK = 0,
+    CVH_ERR_INVALID_ARG = 1,   /* null pointer where one is required, negative size, ... */
+    CVH_ERR_UNSUPPORTED = 2,   /* head_dim / GQA ratio / block size / dtype not compiled */
+    CVH_ERR_WORKSPACE = 3,     /* workspace missing or smaller than required */
+    CVH_ERR_LAUNCH = 4         /* hipGetLastError() after a launch was not hipSuccess */
+};
+
+enum { CVH_SCALE_PER_TOKEN_HEAD = 0, CVH_SCALE_PER_TENSOR = 1 };
+enum { CVH_DTYPE_BF16 = 0, CVH_DTYPE_F16 = 1, CVH_DTYPE_F32 = 2 };
+
+/* ---------------------------------------------------------------------------------------------
+ * Paged FP8 decode attention.
+ * Replaces: void paged_attention_fp8(at::Tensor& out, const at::Tensor& q, const at::Tensor& k_cache,
+ *           const at::Tensor& v_cache, const at::Tensor& k_scale, const at::Tensor& v_scale,
+ *           const at::Tensor& block_tables, const at::Tensor& token_seq,
+ *           const at::Tensor& token_kv_len, double scale)      (kernels/paged_attention.h:5-7,
+ *                                                                kernels/paged_attention.cu:459-473)
+ *   out          bf16 [num_tokens][n_heads][head_dim]
+ *   q            bf16 [num_tokens][n_heads][head_dim]
+ *   block_tables int64 [num_seqs][table_width]; entries past a sequence's last block are ignored
+ *   token_seq    int64 [num_tokens]  row of block_tables for each query token
+ *   token_kv_len int64 [num_tokens]  causal context length of each query token (positions+1);
+ *                                    a token with kv_len <= 0 gets an all-zero output row
+ *   scale        softmax scale (1/sqrt(head_dim) in the reference)
+ * Supported: head_dim in {64,128}; n_heads/n_kv_heads in {1,2,4,8}; block_size a power of two
+ * in [16, 4096]. Queries of one sequence may be several tokens (chunked-prefill continuation).
+ * workspace: device memory of at least cvh_paged_attention_workspace_bytes(...) bytes for the
+ * same arguments (split-K partials). Its contents need no initialisation.
+ * ------------------------------------------------------------------------------------------- */
+int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                            const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                            int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                            int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                            int scale_mode, double scale, void* workspace, size_t workspace_bytes,
+                            cvh_stream_t stream);
+
+/* Same as cvh_paged_attention_fp8 with an explicit split-K chunk: every query token's context is
+ * cut into splits of split_tokens keys (a multiple of 32, >= 64); 0 = automatic choice.
+ * (No reference counterpart for the knob: the reference hard-codes its split heuristic,
+ *  kernels/paged_attention.cu:403-409; tests use it to prove split invariance.) */
+int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                               const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                               int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                               int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                               int scale_mode, double scale, int split_tokens, void* workspace,
+                               size_t workspace_bytes, cvh_stream_t stream);
+
+/* Workspace bytes needed by the calls above (replaces the per-call at::empty of
+ * kernels/paged_attention.cu:415-421, which cannot run under graph capture). */
+size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                           int64_t table_width, int block_size, int split_tokens);
+
+/* The split chunk (keys per split) the automatic policy picks for these shapes. */
+int cvh_paged_attention_split_tokens(int64_t num_tokens, int n_kv_heads, int64_t table_width, int block_size);
+
+/* ---------------------------------------------------------------------------------------------
+ * RMSNorm family. Replaces fused::rms_norm / fused::add_rms_norm (kernels/fused_ops.h:7-9,
+ * kernels/fused_ops.cu:61-98,226-244). Rows are num_rows x dim, contiguous, of `dtype`.
+ *   rms_norm    : out = rnd(rnd(x * inv) * w),  inv = 1/sqrt(sum(x^2)/dim + eps)
+ *   add_rms_norm: v = rnd(resid + x); resid <- v (in place); out as above from v
+ * dim must be a multiple of 8.
+ * ------------------------------------------------------------------------------------------- */
+int cvh_rms_norm(void* out, const void* x, const void* w, int64_t num_rows, int dim, double eps, int dtype,
+                 cvh_stream_t stream);
+int cvh_add_rms_norm(void* resid, const void* x, const void* w, void* out, int64_t num_rows, int dim, double eps,
+                     int dtype, cvh_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Per-head QK-RMSNorm + neox RoPE + FP8 e4m3 quantise-and-scatter of K/V into the paged cache.
+ * Replaces fused::qk_norm_rope_kv_write_fp8 (kernels/fused_ops.h:11-15, fused_ops.cu:104-207,246-259).
+ *   q_out     bf16 [num_tokens][n_heads][head_dim]
+ *   qkv       bf16 [num_tokens][(n_heads + 2*n_kv_heads) * head_dim]  (Q heads, then K, then V)
+ *   q_norm, k_norm  bf16 [head_dim]
+ *   cos_t, sin_t    float32 [max_position][head_dim/2]
+ *   positions int64 [num_tokens]
+ *   slots     int64 [num_tokens]; slots[t] < 0 => no K/V byte and no scale is written for t
+ *             (extension: the reference writes unconditionally, kernels/fused_ops.cu:123)
+ *   k_dense, v_dense  bf16 [num_tokens][n_kv_heads][head_dim] or NULL (reference's optional
+ *             dense copies for the prefill path, kernels/fused_ops.cu:137-141,186-190)
+ *   CVH_SCALE_PER_TOKEN_HEAD: scale = max(amax,1e-8)/448 per (token, kv head), written to
+ *             k_scale/v_scale; CVH_SCALE_PER_TENSOR: k_scale[0]/v_scale[0] are read, not written.
+ * head_dim in {64,128}; block_size a power of two in [16, 4096].
+ * ------------------------------------------------------------------------------------------- */
+int cvh_qk_norm_rope_kv_write_fp8(void* q_out, const void* qkv, const void* q_norm, const void* k_norm,
+                                  const float* cos_t, const float* sin_t, const int64_t* positions,
+                                  const int64_t* slots, uint8_t* k_cache, uint8_t* v_cache, float* k_scale,
+                                  float* v_scale, void* k_dense, void* v_dense, int64_t num_tokens, int n_heads,
+                                  int n_kv_heads, int head_dim, int block_size, int scale_mode, double eps,
+                                  cvh_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Per-token metadata of a ragged batch. Replaces the torch ops of Qwen3::forward_backbone
+ * (model/model_architecture.cpp:137-147):
+ *   token_seq[t] = #{ j in 1..num_seqs : cu_seqlens[j] <= t }   (searchsorted right)
+ *   slot[t]      = block_tables[seq][pos/BS]*BS + pos%BS,  pos = positions[t]
+ *   kv_len[t]    = pos + 1
+ * Tokens past cu_seqlens[num_seqs] (padding) and tokens whose table entry is negative get
+ * token_seq = -1, slot = -1, kv_len = 0. Any output pointer may be NULL.
+ * ------------------------------------------------------------------------------------------- */
+int cvh_build_token_metadata(const int64_t* cu_seqlens, int64_t num_seqs, const int64_t* positions,
+                             int64_t num_tokens, const int64_t* block_tables, int64_t table_width,
+                             int block_size, int64_t* token_seq, int64_t* slots, int64_t* token_kv_len,
+                             cvh_stream_t stream);
+
+/* Host-side RoPE tables (host pointers): inv_freq_i = 1/theta^(2i/head_dim) and
+ * angle = pos*inv_freq in double, cos/sin in double, stored as float32 [max_position][head_dim/2].
+ * Replaces Qwen3::build_rope_tables (model/model_architecture.cpp:67-75). */
+int cvh_rope_tables_host(float* cos_t, float* sin_t, int64_t max_position, int head_dim, double theta);
+
+/* OCP e4m3fn quantiser (round to nearest even, saturate to +-448, NaN -> 0x7F) of n floats:
+ * dst[i] = e4m3(src[i] * inv_scale). The same encoder the cache writer uses
+ * (reference: __nv_cvt_float_to_fp8(x, __NV_SATFINITE, __NV_E4M3), kernels/fused_ops.cu:42-44). */
+int cvh_fp8_e4m3_quantize(uint8_t* dst, const float* src, int64_t n, float inv_scale, cvh_stream_t stream);
+
+/* Library version string (static storage). */
+const char* cvh_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CPPVLLM_HIP_H */

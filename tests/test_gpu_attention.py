@@ -1,0 +1,173 @@
+"""GPU parity of the FP8 paged decode attention against the CPU oracle, through the C ABI.
+
+Bar: max-abs 2e-2 and mean-abs 2e-3 on the bf16 outputs (the build's stated tolerance).
+Covers BASELINE configs 1 (both scale modes), 3 (full headline size), 4 and 4b (long contexts,
+split-K, shared prefix blocks, outliers), the reference's 16-token blocks, GQA ratios 1/2/4/8,
+head_dim 64, ragged and boundary lengths, chunked-prefill continuation rows, empty contexts,
+split-count invariance and physical-block permutation invariance."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cppvllm_amd import ops, workloads
+from tests._util import assert_close_bf16, bits, np_, say
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def run_gpu(b, split_tokens=0):
+    out = torch.empty_like(b["q"])
+    ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                            b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
+                            split_tokens=split_tokens)
+    torch.cuda.synchronize()
+    return bits(out)
+
+
+def run_oracle(orc, b, rows=None):
+    H, KV, HD, BS = b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
+    mode = orc.PER_TENSOR if b["k_scale"].numel() == 1 else orc.PER_TOKEN_HEAD
+    tseq, tlen, q = np_(b["token_seq"]), np_(b["token_kv_len"]), np_(b["q"])
+    if rows is not None:
+        tseq, tlen, q = tseq[rows].copy(), tlen[rows].copy(), q[rows].copy()
+    return orc.paged_attention_fp8(q, np_(b["k_cache"]), np_(b["v_cache"]), np_(b["k_scale"]), np_(b["v_scale"]),
+                                   np_(b["block_tables"]), tseq, tlen, H, KV, HD, BS, mode, b["scale"])
+
+
+def synth(seed, lens, BS, H=16, KV=8, HD=128, per_tensor=False, queries_per_seq=1):
+    """Random quantised cache + q; optional several query tokens per sequence (chunked prefill:
+    the last `queries_per_seq` positions of each context, causal kv_len = pos + 1)."""
+    g = torch.Generator().manual_seed(seed)
+    nblk = [math.ceil(L / BS) for L in lens]
+    nb = sum(nblk) + 3
+    perm = torch.randperm(nb, generator=g)
+    W = max(nblk)
+    table = torch.full((len(lens), W), -1, dtype=torch.int64)
+    p = 0
+    for i, n in enumerate(nblk):
+        table[i, :n] = perm[p:p + n]
+        p += n
+    x = torch.randn((nb, BS, KV, HD), generator=g)
+    y = torch.randn((nb, BS, KV, HD), generator=g)
+    kc, ks = workloads.quantize_blocks(x, per_tensor)
+    vc, vs = workloads.quantize_blocks(y, per_tensor)
+    tseq, tlen = [], []
+    for i, L in enumerate(lens):
+        for j in range(min(queries_per_seq, L)):
+            tseq.append(i)
+            tlen.append(L - j)
+    T = len(tseq)
+    q = torch.randn((T, H, HD), generator=g).to(torch.bfloat16)
+    b = {"q": q, "k_cache": kc, "v_cache": vc, "k_scale": ks, "v_scale": vs, "block_tables": table,
+         "token_seq": torch.tensor(tseq, dtype=torch.int64), "token_kv_len": torch.tensor(tlen, dtype=torch.int64),
+         "block_size": BS, "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "scale": 1 / math.sqrt(HD)}
+    return b
+
+
+def dev(b):
+    return {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in b.items()}
+
+
+@pytest.mark.parametrize("per_tensor", [True, False])
+def test_config1(orc, per_tensor):
+    say(f"config1 per_tensor={per_tensor}")
+    b = workloads.config1(device="cpu", per_tensor=per_tensor)
+    want = run_oracle(orc, b)
+    got = run_gpu(dev(b))
+    assert_close_bf16(got, want)
+
+
+@pytest.mark.parametrize("BS,H,KV,HD,per_tensor", [
+    (16, 16, 8, 128, False), (16, 16, 8, 128, True), (256, 16, 8, 128, False), (32, 8, 8, 128, False),
+    (64, 32, 8, 128, False), (16, 64, 8, 128, False), (16, 8, 2, 64, False), (128, 16, 4, 64, True),
+])
+def test_shapes_and_boundaries(orc, BS, H, KV, HD, per_tensor):
+    lens = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 255, 256, 257, 511, 777, 1030]
+    say(f"shapes BS={BS} H={H} KV={KV} HD={HD} per_tensor={per_tensor}")
+    b = synth(BS * 7 + H + KV + HD, lens, BS, H, KV, HD, per_tensor)
+    want = run_oracle(orc, b)
+    got = run_gpu(dev(b))
+    assert_close_bf16(got, want)
+
+
+@pytest.mark.parametrize("split", [64, 96, 256, 2048])
+def test_split_invariance(orc, split):
+    say(f"split invariance split_tokens={split}")
+    b = synth(11, [70, 600, 1500, 2100, 3000], 16)
+    db = dev(b)
+    base = run_gpu(db, 0)
+    got = run_gpu(db, split)
+    assert_close_bf16(got, base, max_abs=8e-3, mean_abs=5e-4)
+    assert_close_bf16(got, run_oracle(orc, b))
+
+
+def test_chunked_prefill_rows(orc):
+    say("chunked prefill continuation rows")
+    b = synth(21, [40, 300, 1000], 16, queries_per_seq=37)
+    assert_close_bf16(run_gpu(dev(b)), run_oracle(orc, b))
+
+
+def test_empty_context_rows_are_zero(orc):
+    say("kv_len 0 rows")
+    b = synth(5, [100, 50], 16)
+    b["token_kv_len"][1] = 0
+    got = run_gpu(dev(b))
+    assert (got[1] == 0).all()
+    assert_close_bf16(got[:1], run_oracle(orc, b, rows=[0]))
+
+
+def test_block_permutation_invariance_bitwise():
+    say("physical block permutation invariance")
+    b = synth(31, [500, 900, 17], 16)
+    base = run_gpu(dev(b))
+    nb = b["k_cache"].shape[0]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(1))
+    inv = torch.argsort(perm)
+    b2 = dict(b)
+    for k in ("k_cache", "v_cache", "k_scale", "v_scale"):
+        b2[k] = b[k][inv].contiguous()
+    t = b["block_tables"]
+    b2["block_tables"] = torch.where(t >= 0, perm[t.clamp_min(0)], t)
+    assert np.array_equal(run_gpu(dev(b2)), base)
+
+
+def test_config3_full(orc):
+    say("config3 full: 256 seqs, BS=256, per-token scales")
+    b = workloads.config3(device="cpu")
+    want = run_oracle(orc, b)
+    got = run_gpu(dev(b))
+    say("config3 errors (max, mean):", assert_close_bf16(got, want))
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_config4_long_context(orc, shared):
+    say(f"config4 64 seqs log-U(4k,32k) shared_prefix={shared}")
+    b = workloads.config4(device=DEV, shared_prefix=shared)
+    got = run_gpu(b)
+    assert np.isfinite((got.astype(np.uint32) << 16).view(np.float32)).all()
+    rows = [0, 1, 2, 7, 30, 63]
+    bc = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in b.items()}
+    want = run_oracle(orc, bc, rows=rows)
+    assert_close_bf16(got[rows], want)
+    if shared:
+        t = bc["block_tables"]
+        assert (t[0, :8] == t[2, :8]).all() and (t[0, :8] == t[62, :8]).all()
+
+
+def test_workspace_contract():
+    say("workspace contract")
+    from cppvllm_amd import _lib
+    b = dev(synth(3, [3000, 20], 16))
+    T, H = b["q"].shape[:2]
+    W = b["block_tables"].shape[1]
+    need = _lib.lib().cvh_paged_attention_workspace_bytes(T, H, 8, 128, W, 16, 64)
+    assert need > 0
+    small = torch.empty(need - 4, dtype=torch.uint8, device=DEV)
+    with pytest.raises(_lib.CvhError) as e:
+        ops.paged_attention_fp8(torch.empty_like(b["q"]), b["q"], b["k_cache"], b["v_cache"], b["k_scale"],
+                                b["v_scale"], b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
+                                workspace=small, split_tokens=64)
+    assert e.value.code == _lib.CVH_ERR_WORKSPACE
