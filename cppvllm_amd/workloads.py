@@ -170,15 +170,19 @@ def attention_bytes(kv_lens, n_kv=KV, hd=HD, n_heads=H, per_tensor=False) -> int
 
 
 def fused_batch(seed: int = 1002, device="cpu", T: int = 4096, n_segments: int = 32, bs: int = 256,
-                per_tensor: bool = False):
-    """Config 2: packed ragged batch of T tokens for add_rms_norm and qk_norm_rope_kv_write."""
+                per_tensor: bool = False, pad_rows: int = 64):
+    """Config 2: packed ragged batch of T tokens for add_rms_norm and qk_norm_rope_kv_write.
+
+    Segments (lengths U{16..256}, positions continuing a cached prefix of U{0..1024} tokens) fill
+    at most T - pad_rows rows (the last segment is truncated); the remaining rows are padding with
+    slot -1 and position 0, like the idle rows of a captured decode batch."""
     g = _cpu_gen(seed)
     lens = torch.randint(16, 257, (n_segments,), generator=g).tolist()
     offs = torch.randint(0, 1025, (n_segments,), generator=g).tolist()
     total = 0
     seg = []
     for L, o in zip(lens, offs):
-        L = min(L, T - total)
+        L = min(L, T - pad_rows - total)
         if L <= 0:
             break
         seg.append((L, o))
