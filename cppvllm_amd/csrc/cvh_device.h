@@ -83,22 +83,22 @@ __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
 }
 
 // ---- DPP helpers (within rows of 16 lanes) ---------------------------------------------------
-// Sum with the lane at (lane ^ 1), (lane ^ 2) inside a quad: quad_perm patterns.
-__device__ __forceinline__ float dpp_xor1(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+// All patterns below give every lane a valid source lane, so bound_ctrl (zero for invalid
+// sources) never applies; setting it lets the compiler fold the move into the consuming VALU op
+// (v_add_f32_dpp / v_max_f32_dpp).
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
-__device__ __forceinline__ float dpp_xor2(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-}
+// lane ^ 1 and lane ^ 2 inside a quad (quad_perm [1,0,3,2] and [2,3,0,1]).
+__device__ __forceinline__ float dpp_xor1(float v) { return dpp<0xB1>(v); }
+__device__ __forceinline__ float dpp_xor2(float v) { return dpp<0x4E>(v); }
 // row_half_mirror: lane i <-> 7-i inside each group of 8. After the xor1/xor2 levels a quad is
 // uniform, so this pairs quad 0 with quad 1 exactly like an xor-4 exchange would.
-__device__ __forceinline__ float dpp_half_mirror(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
-}
+__device__ __forceinline__ float dpp_half_mirror(float v) { return dpp<0x141>(v); }
 // row_mirror: lane i <-> 15-i inside each row of 16 (an xor-8 exchange once halves are uniform).
-__device__ __forceinline__ float dpp_mirror(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
-}
+__device__ __forceinline__ float dpp_mirror(float v) { return dpp<0x140>(v); }
+// row_ror:8: lane i <-> (i+8) mod 16 inside each row of 16, i.e. exactly lane ^ 8.
+__device__ __forceinline__ float dpp_xor8(float v) { return dpp<0x128>(v); }
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 

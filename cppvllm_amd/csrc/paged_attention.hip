@@ -10,6 +10,8 @@
 //     instruction covers 8 full key rows (8 x 128 B cache lines, no partial lines);
 //   * a tile is 4 steps = 32 keys; tile t+1's K/V/scale loads are issued before tile t is
 //     computed (register double buffer) to keep >= 8 KB in flight per wave;
+//   * K/V loads are non-temporal (streamed once), and a workgroup carries the waves of 4
+//     consecutive kv heads of one (token, split) so whole 1 KB slot rows are read together;
 //   * FP8 -> f32 with the hardware OCP converter (v_cvt_pk_f32_fp8, exact for finite codes);
 //   * q.k partial dots reduce over the 8 lanes of a key with DPP (quad_perm, half-mirror);
 //   * softmax in base 2 (scale*log2(e) folded into q) with a lazy running max: the
@@ -24,6 +26,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "cvh_device.h"
 
@@ -34,7 +37,20 @@ constexpr int kTileKeys = 32;      // keys per wave per tile (4 steps x 8 key gr
 constexpr int kSteps = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;   // log2 units: stale max tolerated up to p = 2^8
+constexpr float kMinusHuge = -1e30f;
 
+// K/V rows are read exactly once per launch: non-temporal loads keep them from displacing
+// reusable lines (block tables, q, partials) in L2 / MALL. Measured: -8% kernel time at config 3.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 nt_load(const uint4* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 nt_load(const uint2* p) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    return make_uint2(v[0], v[1]);
+}
 template <int HD> struct KvVec;
 template <> struct KvVec<128> {
     using T = uint4;
@@ -62,27 +78,44 @@ __device__ __forceinline__ float group8_sum(float v) {
     v = v + dpp_half_mirror(v);
     return v;
 }
-// xor-8 exchange inside a row of 16 (row_ror:8).
-__device__ __forceinline__ float dpp_ror8(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+// Exchange across rows of 16 / halves of 32 lanes with the gfx950 permlane swaps (no LDS, no
+// LGKM counter traffic): with both operands = v, the pair returned holds, per lane, its own
+// value and its xor-16 (resp. xor-32) partner's value.
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // Combine the 8 key groups (sum), result in every lane; lanes with equal sub get equal values.
 __device__ __forceinline__ float across_groups_sum(float v) {
-    v = v + dpp_ror8(v);
-    v = v + shfl_xor(v, 16);
-    v = v + shfl_xor(v, 32);
-    return v;
+    v = v + dpp_xor8(v);
+    v = xor16_sum(v);
+    return xor32_sum(v);
 }
 // Max over the whole wave of a value that is already uniform inside each key group.
 __device__ __forceinline__ float across_groups_max(float v) {
-    v = fmaxf(v, dpp_ror8(v));
-    v = fmaxf(v, shfl_xor(v, 16));
-    v = fmaxf(v, shfl_xor(v, 32));
-    return v;
+    v = fmaxf(v, dpp_xor8(v));
+    v = xor16_max(v);
+    return xor32_max(v);
 }
 
-template <int HD, int REP, int SM>
-__global__ __launch_bounds__(64) void paged_decode_kernel(
+// ONE_BLOCK: block_size >= 32, so a 32-key tile never straddles two cache blocks and one
+// block-table lookup serves the whole tile. Otherwise (block_size 16) each 8-key step still lies
+// in a single block, looked up per step. Lookups are wave-uniform scalar loads; the per-lane
+// address is a 32-bit offset from a scalar block base.
+template <int HD, int REP, int SM, bool ONE_BLOCK>
+__global__ __launch_bounds__(256) void paged_decode_kernel(
         uint16_t* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
         const uint16_t* __restrict__ q, const uint8_t* __restrict__ k_cache, const uint8_t* __restrict__ v_cache,
         const float* __restrict__ k_scale, const float* __restrict__ v_scale, const int64_t* __restrict__ block_tables,
@@ -91,18 +124,20 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
     using V = KvVec<HD>;
     using VT = typename V::T;
     constexpr int E = V::kElems;                 // elements of HD owned per lane
+    // A workgroup holds the waves of (blockDim.x/64) consecutive kv heads of one (token, split):
+    // together they read whole slot rows, so the HBM pages they touch are read at the same time.
     const int t = blockIdx.x;
-    const int g = blockIdx.y;
+    const int g = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int split = blockIdx.z;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     const int grp = lane >> 3;
     const int sub = lane & 7;
     const int H = n_kv * REP;
 
-    int64_t kv_len = token_kv_len[t];
+    int64_t kv64 = token_kv_len[t];
     const int64_t cap = table_width << log2_bs;  // never read past the block table row
-    if (kv_len > cap) kv_len = cap;
-    if (kv_len <= 0) {                           // empty context: zero output (reference: 0/0)
+    if (kv64 > cap) kv64 = cap;
+    if (kv64 <= 0) {                             // empty context: zero output (reference: 0/0)
         if (split == 0) {
 #pragma unroll
             for (int r = 0; r < REP; ++r) {
@@ -112,14 +147,17 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         }
         return;
     }
-    const int64_t ntiles = (kv_len + kTileKeys - 1) / kTileKeys;
-    const int64_t nsplit = (ntiles + split_tiles - 1) / split_tiles;
+    const int kv_len = static_cast<int>(kv64);   // the host limits table_width*block_size < 2^31
+    const int ntiles = (kv_len + kTileKeys - 1) / kTileKeys;
+    const int nsplit = (ntiles + split_tiles - 1) / split_tiles;
     if (split >= nsplit) return;
-    const int64_t tile_begin = (int64_t)split * split_tiles;
-    const int64_t tile_end = min(ntiles, tile_begin + split_tiles);
+    const int tile_begin = split * split_tiles;
+    const int tile_end = min(ntiles, tile_begin + split_tiles);
     const int64_t* table = block_tables + token_seq[t] * table_width;
-    const int64_t row_bytes = (int64_t)n_kv * HD;    // bytes of one cache slot (all kv heads)
+    const uint32_t row_bytes = static_cast<uint32_t>(n_kv) * HD;    // bytes of one slot (all kv heads)
+    const int64_t blk_bytes = static_cast<int64_t>(row_bytes) << log2_bs;
     const int bs_mask = (1 << log2_bs) - 1;
+    const uint32_t lane_col = g * HD + sub * E;  // byte column of this lane inside a slot row
 
     // ---- q slice for the REP heads of this kv head, pre-scaled by scale*log2(e) [*k_scale]
     const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? q_scale * k_scale[0] : q_scale;
@@ -139,38 +177,55 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         }
     }
 
+    // Running max per key group (lanes 8k..8k+7 agree on it): no cross-group exchange per tile.
+    // Starts at a finite floor so that a group whose keys are all masked gives exp2(-inf) = 0.
     float m[REP], l[REP], acc[REP][E];
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-        m[r] = -INFINITY;
+        m[r] = kMinusHuge;
         l[r] = 0.f;
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[r][e] = 0.f;
     }
 
-    // ---- tile loader: K/V slices and per-key scales for keys tile*32 + 8*s + grp
+    // ---- tile loader: K/V slices and per-key scales for keys tile*32 + 8*s + grp.
+    // Keys past kv_len (last tile only) are clamped to key kv_len-1: a valid, finite row whose
+    // score is masked, so no garbage (possibly NaN) cache byte ever reaches the accumulator.
     struct Tile {
         VT k[kSteps], v[kSteps];
         float ks[kSteps], vs[kSteps];
     };
-    auto load_tile = [&](int64_t tile, Tile& tl) {
-        const int64_t p0 = tile * kTileKeys;
-        const int64_t last = min(p0 + kTileKeys - 1, kv_len - 1);
-        const int64_t bi_lo = p0 >> log2_bs, bi_hi = last >> log2_bs;   // block_size >= 16: <= 2 blocks
-        const int64_t ph_lo = max(table[bi_lo], int64_t{0});
-        const int64_t ph_hi = max(table[bi_hi], int64_t{0});
+    // Physical blocks of a tile: `lo` for its first 16 keys, `hi` for the last 16 (equal unless
+    // block_size == 16). Both wave-uniform (scalar loads); looked up one tile ahead of use.
+    struct Phys {
+        int64_t lo, hi;
+    };
+    auto lookup = [&](int tile) -> Phys {
+        tile = min(tile, tile_end - 1);
+        const int p0 = tile * kTileKeys;
+        const int64_t lo = max(table[p0 >> log2_bs], int64_t{0});
+        if constexpr (ONE_BLOCK) return {lo, lo};
+        const int64_t hi = max(table[min(p0 + 16, kv_len - 1) >> log2_bs], int64_t{0});
+        return {lo, hi};
+    };
+    auto load_tile = [&](int tile, Tile& tl, Phys ph2) {
+        const int p0 = tile * kTileKeys;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
-            const int64_t pos = min(p0 + 8 * s + grp, kv_len - 1);         // masked keys re-read a valid row
-            const int64_t ph = ((pos >> log2_bs) == bi_lo) ? ph_lo : ph_hi;
-            const int off = static_cast<int>(pos & bs_mask);
-            const int64_t byte = (((ph << log2_bs) + off) * row_bytes) + g * HD + sub * E;
-            tl.k[s] = *reinterpret_cast<const VT*>(k_cache + byte);
-            tl.v[s] = *reinterpret_cast<const VT*>(v_cache + byte);
+            const int64_t ph = (ONE_BLOCK || s < 2) ? ph2.lo : ph2.hi;
+            const int pos = min(p0 + 8 * s + grp, kv_len - 1);
+            const uint32_t in_blk = static_cast<uint32_t>(pos & bs_mask);
+            const uint32_t off = in_blk * row_bytes + lane_col;
+            const uint8_t* kb = k_cache + ph * blk_bytes;    // uniform block base
+            const uint8_t* vb = v_cache + ph * blk_bytes;
+            tl.k[s] = nt_load(reinterpret_cast<const VT*>(kb + off));
+            tl.v[s] = nt_load(reinterpret_cast<const VT*>(vb + off));
             if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
-                const int64_t sidx = ((ph * n_kv + g) << log2_bs) + off;
-                tl.ks[s] = k_scale[sidx];
-                tl.vs[s] = v_scale[sidx];
+                const int64_t sbase = (ph * n_kv + g) << log2_bs;
+                const float* ksb = k_scale + sbase;             // uniform scale-row base
+                const float* vsb = v_scale + sbase;
+                tl.ks[s] = ksb[in_blk];
+                tl.vs[s] = vsb[in_blk];
             } else {
                 tl.ks[s] = 1.f;
                 tl.vs[s] = 1.f;
@@ -178,8 +233,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         }
     };
 
-    auto compute_tile = [&](int64_t tile, const Tile& tl) {
-        const int64_t p0 = tile * kTileKeys;
+    auto compute = [&](int tile, const Tile& tl) {
+        const int p0 = tile * kTileKeys;
         float sc[REP][kSteps];
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
@@ -198,26 +253,29 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
             const bool valid = (p0 + 8 * s + grp) < kv_len;
 #pragma unroll
             for (int r = 0; r < REP; ++r) {
-                const float d = group8_sum(sc[r][s]);
-                sc[r][s] = valid ? d * tl.ks[s] : -INFINITY;
+                float d = group8_sum(sc[r][s]);
+                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) d *= tl.ks[s];
+                sc[r][s] = valid ? d : -INFINITY;
             }
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-            float mt = fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3]));
-            mt = across_groups_max(mt);
-            if (mt > m[r] + kRescaleThreshold) {
-                const float c = exp2f(m[r] - mt);
+            const float mt = fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3]));
+            const bool need = mt > m[r] + kRescaleThreshold;    // per key group
+            if (__builtin_amdgcn_ballot_w64(need) != 0) {      // wave-uniform; rare after tile 0
+                const float mn = need ? mt : m[r];
+                const float c = __builtin_amdgcn_exp2f(m[r] - mn);
                 l[r] *= c;
 #pragma unroll
                 for (int e = 0; e < E; ++e) acc[r][e] *= c;
-                m[r] = mt;
+                m[r] = mn;
             }
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) {
-                const float p = exp2f(sc[r][s] - m[r]);
+                const float p = __builtin_amdgcn_exp2f(sc[r][s] - m[r]);
                 l[r] += p;
-                sc[r][s] = p * tl.vs[s];
+                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) sc[r][s] = p * tl.vs[s];
+                else sc[r][s] = p;
             }
         }
 #pragma unroll
@@ -233,24 +291,35 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(
         }
     };
 
-    // Register double buffer, unrolled by two so no tile is ever copied between buffers.
+    // Register double buffer, unrolled by two so no tile is ever copied between buffers; the
+    // block-table lookup runs one tile ahead of the loads that use it. The prefetch is issued
+    // unconditionally (past the end it re-reads the last tile, an L2 hit) so that it sits in
+    // straight-line code and the wait before each compute only covers the tile it consumes.
     Tile ta, tb;
-    load_tile(tile_begin, ta);
-    for (int64_t tile = tile_begin; tile < tile_end; tile += 2) {
-        if (tile + 1 < tile_end) load_tile(tile + 1, tb);
-        compute_tile(tile, ta);
+    Phys pa_ = lookup(tile_begin);
+    Phys pb_ = lookup(tile_begin + 1);
+    load_tile(tile_begin, ta, pa_);
+    for (int tile = tile_begin;; tile += 2) {
+        load_tile(min(tile + 1, tile_end - 1), tb, pb_);
+        pa_ = lookup(tile + 2);
+        compute(tile, ta);
         if (tile + 1 >= tile_end) break;
-        if (tile + 2 < tile_end) load_tile(tile + 2, ta);
-        compute_tile(tile + 1, tb);
+        load_tile(min(tile + 2, tile_end - 1), ta, pa_);
+        pb_ = lookup(tile + 3);
+        compute(tile + 1, tb);
+        if (tile + 2 >= tile_end) break;
     }
 
-    // ---- combine the 8 key groups (shared running max => plain sums)
+    // ---- combine the 8 key groups: rescale each to the wave max, then sum
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
+        const float M = across_groups_max(m[r]);
+        const float c = __builtin_amdgcn_exp2f(m[r] - M);
+        m[r] = M;
         // l is uniform inside a group (every lane of a group sums the same p's); sum over groups.
-        l[r] = across_groups_sum(l[r]);
+        l[r] = across_groups_sum(l[r] * c);
 #pragma unroll
-        for (int e = 0; e < E; ++e) acc[r][e] = across_groups_sum(acc[r][e]);
+        for (int e = 0; e < E; ++e) acc[r][e] = across_groups_sum(acc[r][e] * c);
     }
     if (grp != 0) return;
 
@@ -354,23 +423,29 @@ size_t ws_bytes(int64_t T, int H, int HD, int64_t splits) {
 }
 
 template <int HD, int REP, int SM>
-void launch(dim3 grid, hipStream_t s, void* out, float* pa, float* pm, const void* q, const uint8_t* kc,
+void launch(dim3 grid, int threads, hipStream_t s, void* out, float* pa, float* pm, const void* q, const uint8_t* kc,
             const uint8_t* vc, const float* ks, const float* vs, const int64_t* bt, int64_t tw, const int64_t* ts,
             const int64_t* tl, int n_kv, int lg, int split_tiles, int max_splits, float qs) {
-    paged_decode_kernel<HD, REP, SM><<<grid, 64, 0, s>>>(static_cast<uint16_t*>(out), pa, pm,
-                                                         static_cast<const uint16_t*>(q), kc, vc, ks, vs, bt, tw, ts,
-                                                         tl, n_kv, lg, split_tiles, max_splits, qs);
+    if (lg >= 5)
+        paged_decode_kernel<HD, REP, SM, true><<<grid, threads, 0, s>>>(static_cast<uint16_t*>(out), pa, pm,
+                                                                   static_cast<const uint16_t*>(q), kc, vc, ks, vs, bt,
+                                                                   tw, ts, tl, n_kv, lg, split_tiles, max_splits, qs);
+    else
+        paged_decode_kernel<HD, REP, SM, false><<<grid, threads, 0, s>>>(static_cast<uint16_t*>(out), pa, pm,
+                                                                    static_cast<const uint16_t*>(q), kc, vc, ks, vs,
+                                                                    bt, tw, ts, tl, n_kv, lg, split_tiles, max_splits,
+                                                                    qs);
 }
 
 template <int HD, int SM>
-bool launch_rep(int rep, dim3 grid, hipStream_t s, void* out, float* pa, float* pm, const void* q,
+bool launch_rep(int rep, dim3 grid, int threads, hipStream_t s, void* out, float* pa, float* pm, const void* q,
                 const uint8_t* kc, const uint8_t* vc, const float* ks, const float* vs, const int64_t* bt, int64_t tw,
                 const int64_t* ts, const int64_t* tl, int n_kv, int lg, int st, int ms, float qs) {
     switch (rep) {
-        case 1: launch<HD, 1, SM>(grid, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
-        case 2: launch<HD, 2, SM>(grid, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
-        case 4: launch<HD, 4, SM>(grid, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
-        case 8: launch<HD, 8, SM>(grid, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
+        case 1: launch<HD, 1, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
+        case 2: launch<HD, 2, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
+        case 4: launch<HD, 4, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
+        case 8: launch<HD, 8, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
         default: return false;
     }
 }
@@ -417,6 +492,7 @@ extern "C" int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_
     if (!valid_split(split_tokens)) return CVH_ERR_INVALID_ARG;
     const int64_t ms = num_splits_max(table_width, block_size, split_tokens);
     if (ms > 65535) return CVH_ERR_UNSUPPORTED;
+    if (table_width > (int64_t{0x7fffffff} >> lg)) return CVH_ERR_UNSUPPORTED;   // contexts < 2^31 keys
     const size_t need = ws_bytes(num_tokens, n_heads, head_dim, ms);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return CVH_ERR_WORKSPACE;
     float* pa = static_cast<float*>(workspace);
@@ -426,24 +502,26 @@ extern "C" int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_
     // device float, so the kernel folds it into q after reading it.
     const float qs = static_cast<float>(scale) * kLog2e;
     auto s = reinterpret_cast<hipStream_t>(stream);
-    const dim3 grid(static_cast<unsigned>(num_tokens), static_cast<unsigned>(n_kv_heads), static_cast<unsigned>(ms));
+    const int wpg = (n_kv_heads % 4 == 0) ? 4 : (n_kv_heads % 2 == 0) ? 2 : 1;   // waves (kv heads) per group
+    const dim3 grid(static_cast<unsigned>(num_tokens), static_cast<unsigned>(n_kv_heads / wpg),
+                    static_cast<unsigned>(ms));
     const int st = split_tokens / kTileKeys;
     bool ok;
     if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD) {
-        ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, s, out, pa, pm, q, k_cache, v_cache,
+        ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
                                                                         k_scale, v_scale, block_tables, table_width,
                                                                         token_seq, token_kv_len, n_kv_heads, lg, st,
                                                                         static_cast<int>(ms), qs)
-                             : launch_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, s, out, pa, pm, q, k_cache, v_cache,
+                             : launch_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
                                                                        k_scale, v_scale, block_tables, table_width,
                                                                        token_seq, token_kv_len, n_kv_heads, lg, st,
                                                                        static_cast<int>(ms), qs);
     } else {
-        ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TENSOR>(rep, grid, s, out, pa, pm, q, k_cache, v_cache,
+        ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TENSOR>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
                                                                     k_scale, v_scale, block_tables, table_width,
                                                                     token_seq, token_kv_len, n_kv_heads, lg, st,
                                                                     static_cast<int>(ms), qs)
-                             : launch_rep<64, CVH_SCALE_PER_TENSOR>(rep, grid, s, out, pa, pm, q, k_cache, v_cache,
+                             : launch_rep<64, CVH_SCALE_PER_TENSOR>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
                                                                    k_scale, v_scale, block_tables, table_width,
                                                                    token_seq, token_kv_len, n_kv_heads, lg, st,
                                                                    static_cast<int>(ms), qs);
