@@ -171,3 +171,49 @@ def test_workspace_contract():
                                 b["v_scale"], b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
                                 workspace=small, split_tokens=64)
     assert e.value.code == _lib.CVH_ERR_WORKSPACE
+
+
+def test_workspace_reused():
+    say("workspace reuse: two calls with one workspace")
+    from cppvllm_amd import _lib
+    b = dev(synth(41, [3000, 700, 64, 1500], 16))
+    T, H = b["q"].shape[:2]
+    W = b["block_tables"].shape[1]
+    ws = ops.paged_attention_workspace(T, H, 8, 128, W, 16, 64, DEV)
+    outs = []
+    for _ in range(2):
+        out = torch.empty_like(b["q"])
+        ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                                b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"], workspace=ws,
+                                split_tokens=64)
+        torch.cuda.synchronize()
+        outs.append(bits(out))
+    assert np.array_equal(outs[0], outs[1])
+    _ = _lib  # noqa
+
+
+def test_graph_replay_matches_eager():
+    say("hip graph capture + 3 replays")
+    b = dev(synth(43, [900, 2500, 40, 333], 16))
+    T, H = b["q"].shape[:2]
+    W = b["block_tables"].shape[1]
+    ws = ops.paged_attention_workspace(T, H, 8, 128, W, 16, 0, DEV)
+    eager = run_gpu(b)
+    out = torch.empty_like(b["q"])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):   # warm-up on the capture stream
+        ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                                b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"], workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                                b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"], workspace=ws)
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), eager), f"replay {i} differs from eager"
+        _ = run_gpu(b)   # eager work between replays
