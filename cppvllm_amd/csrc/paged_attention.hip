@@ -39,18 +39,31 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;   // log2 units: stale max tolerated up to p = 2^8
 constexpr float kMinusHuge = -1e30f;
 
-// K/V rows are read exactly once per launch: non-temporal loads keep them from displacing
-// reusable lines (block tables, q, partials) in L2 / MALL. Measured: -8% kernel time at config 3.
+// K/V rows and scales go through raw buffer loads: the descriptor's record count bounds every
+// access, so a tile that must not be read (the prefetch issued past a split's last tile) is given
+// a zero-size descriptor and returns zeros without touching memory. All K/V/scale loads carry the
+// non-temporal hint: each byte is read once per launch, so it should not displace reusable lines
+// (block tables, q, partials) in L2 / MALL (measured: -8% kernel time at config 3).
+constexpr int kBufferWord3 = 0x00020000;      // raw buffer, 32-bit data format (gfx9 encoding)
+constexpr int kNonTemporal = 2;               // cache-policy bits of the load: nt
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint4 nt_load(const uint4* p) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
+}
+template <typename VT> __device__ __forceinline__ VT buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ uint4 buf_load<uint4>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNonTemporal);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ uint2 nt_load(const uint2* p) {
-    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+template <> __device__ __forceinline__ uint2 buf_load<uint2>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNonTemporal);
     return make_uint2(v[0], v[1]);
 }
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNonTemporal));
+}
+
 template <int HD> struct KvVec;
 template <> struct KvVec<128> {
     using T = uint4;
@@ -127,7 +140,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     // A workgroup holds the waves of (blockDim.x/64) consecutive kv heads of one (token, split):
     // together they read whole slot rows, so the HBM pages they touch are read at the same time.
     const int t = blockIdx.x;
-    const int g = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // wave-uniform by construction; readfirstlane tells the compiler so (scalar descriptors)
+    const int g = __builtin_amdgcn_readfirstlane(blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6));
     const int split = blockIdx.z;
     const int lane = threadIdx.x & 63;
     const int grp = lane >> 3;
@@ -208,24 +222,29 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
         const int64_t hi = max(table[min(p0 + 16, kv_len - 1) >> log2_bs], int64_t{0});
         return {lo, hi};
     };
-    auto load_tile = [&](int tile, Tile& tl, Phys ph2) {
+    // live = false: the prefetch past the split's last tile; zero-size descriptors, no traffic.
+    const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
+    const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
+    auto load_tile = [&](int tile, Tile& tl, Phys ph2, bool live) {
         const int p0 = tile * kTileKeys;
+        const uint32_t lv = static_cast<uint32_t>(live);               // arithmetic, not a branch
+        const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
             const int64_t ph = (ONE_BLOCK || s < 2) ? ph2.lo : ph2.hi;
             const int pos = min(p0 + 8 * s + grp, kv_len - 1);
             const uint32_t in_blk = static_cast<uint32_t>(pos & bs_mask);
             const uint32_t off = in_blk * row_bytes + lane_col;
-            const uint8_t* kb = k_cache + ph * blk_bytes;    // uniform block base
-            const uint8_t* vb = v_cache + ph * blk_bytes;
-            tl.k[s] = nt_load(reinterpret_cast<const VT*>(kb + off));
-            tl.v[s] = nt_load(reinterpret_cast<const VT*>(vb + off));
+            const __amdgpu_buffer_rsrc_t kr = make_rsrc(k_cache + ph * blk_bytes, kv_rec);
+            const __amdgpu_buffer_rsrc_t vr = make_rsrc(v_cache + ph * blk_bytes, kv_rec);
+            tl.k[s] = buf_load<VT>(kr, off);
+            tl.v[s] = buf_load<VT>(vr, off);
             if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
                 const int64_t sbase = (ph * n_kv + g) << log2_bs;
-                const float* ksb = k_scale + sbase;             // uniform scale-row base
-                const float* vsb = v_scale + sbase;
-                tl.ks[s] = ksb[in_blk];
-                tl.vs[s] = vsb[in_blk];
+                const __amdgpu_buffer_rsrc_t ksr = make_rsrc(k_scale + sbase, s_rec);
+                const __amdgpu_buffer_rsrc_t vsr = make_rsrc(v_scale + sbase, s_rec);
+                tl.ks[s] = buf_load_f32(ksr, in_blk * 4u);
+                tl.vs[s] = buf_load_f32(vsr, in_blk * 4u);
             } else {
                 tl.ks[s] = 1.f;
                 tl.vs[s] = 1.f;
@@ -293,18 +312,18 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
 
     // Register double buffer, unrolled by two so no tile is ever copied between buffers; the
     // block-table lookup runs one tile ahead of the loads that use it. The prefetch is issued
-    // unconditionally (past the end it re-reads the last tile, an L2 hit) so that it sits in
-    // straight-line code and the wait before each compute only covers the tile it consumes.
+    // unconditionally (past the end with zero-size descriptors) so that it sits in straight-line
+    // code and the wait before each compute only covers the tile it consumes.
     Tile ta, tb;
     Phys pa_ = lookup(tile_begin);
     Phys pb_ = lookup(tile_begin + 1);
-    load_tile(tile_begin, ta, pa_);
+    load_tile(tile_begin, ta, pa_, true);
     for (int tile = tile_begin;; tile += 2) {
-        load_tile(min(tile + 1, tile_end - 1), tb, pb_);
+        load_tile(min(tile + 1, tile_end - 1), tb, pb_, tile + 1 < tile_end);
         pa_ = lookup(tile + 2);
         compute(tile, ta);
         if (tile + 1 >= tile_end) break;
-        load_tile(min(tile + 2, tile_end - 1), ta, pa_);
+        load_tile(min(tile + 2, tile_end - 1), ta, pa_, tile + 2 < tile_end);
         pb_ = lookup(tile + 3);
         compute(tile + 1, tb);
         if (tile + 2 >= tile_end) break;
@@ -468,13 +487,15 @@ extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_
                                 cvh::num_splits_max(table_width, block_size, split_tokens));
 }
 
-extern "C" int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
-                                          const float* k_scale, const float* v_scale, const int64_t* block_tables,
-                                          int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
-                                          int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                                          int block_size, int scale_mode, double scale, int split_tokens,
-                                          void* workspace, size_t workspace_bytes, cvh_stream_t stream) {
-    using namespace cvh;
+namespace cvh {
+namespace {
+enum Phase { kPhaseSplit = 1, kPhaseMerge = 2, kPhaseBoth = 3 };
+
+int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache, const float* k_scale,
+                    const float* v_scale, const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
+                    const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                    int block_size, int scale_mode, double scale, int split_tokens, void* workspace,
+                    size_t workspace_bytes, cvh_stream_t stream, int phase) {
     if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0) return CVH_ERR_INVALID_ARG;
     if (num_tokens == 0) return CVH_OK;
     if (!out || !q || !k_cache || !v_cache || !k_scale || !v_scale || !block_tables || !token_seq || !token_kv_len)
@@ -506,7 +527,8 @@ extern "C" int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_
     const dim3 grid(static_cast<unsigned>(num_tokens), static_cast<unsigned>(n_kv_heads / wpg),
                     static_cast<unsigned>(ms));
     const int st = split_tokens / kTileKeys;
-    bool ok;
+    bool ok = true;
+    if (phase & kPhaseSplit) {
     if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD) {
         ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
                                                                         k_scale, v_scale, block_tables, table_width,
@@ -526,9 +548,10 @@ extern "C" int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_
                                                                    token_seq, token_kv_len, n_kv_heads, lg, st,
                                                                    static_cast<int>(ms), qs);
     }
+    }
     if (!ok) return CVH_ERR_UNSUPPORTED;
     if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
-    if (ms > 1) {
+    if (ms > 1 && (phase & kPhaseMerge)) {
         const dim3 mgrid(static_cast<unsigned>(n_heads), static_cast<unsigned>(num_tokens));
         auto* o = static_cast<uint16_t*>(out);
         if (head_dim == 128) {
@@ -545,6 +568,29 @@ extern "C" int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
     return CVH_OK;
+}
+}  // namespace
+}  // namespace cvh
+
+#define CVH_PA_ARGS                                                                                                   \
+    out, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq, token_kv_len, num_tokens,      \
+            n_heads, n_kv_heads, head_dim, block_size, scale_mode, scale, split_tokens, workspace, workspace_bytes,  \
+            stream
+#define CVH_PA_PARAMS                                                                                                 \
+    void *out, const void *q, const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,                 \
+            const float *v_scale, const int64_t *block_tables, int64_t table_width, const int64_t *token_seq,        \
+            const int64_t *token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,              \
+            int block_size, int scale_mode, double scale, int split_tokens, void *workspace, size_t workspace_bytes, \
+            cvh_stream_t stream
+
+extern "C" int cvh_paged_attention_fp8_ex(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseBoth);
+}
+extern "C" int cvh_paged_attention_fp8_split_phase(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseSplit);
+}
+extern "C" int cvh_paged_attention_fp8_merge_phase(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseMerge);
 }
 
 extern "C" int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,

@@ -81,6 +81,26 @@ int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_t* k_cache,
                                int scale_mode, double scale, int split_tokens, void* workspace,
                                size_t workspace_bytes, cvh_stream_t stream);
 
+/* The two launches of cvh_paged_attention_fp8_ex, exposed separately (same arguments; run on one
+ * stream, split phase first): the split phase runs the decode kernel, which writes the output of
+ * every token whose context fits one split and (acc, max, sum) partials for the others; the
+ * merge phase combines those partials (no-op when no token can have two splits). Callers use
+ * them to time the decode kernel alone or to interleave other work between the phases.
+ * (No reference counterpart: the reference launches both back to back,
+ *  kernels/paged_attention.cu:423-441.) */
+int cvh_paged_attention_fp8_split_phase(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                        const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                        int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                                        int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                        int block_size, int scale_mode, double scale, int split_tokens,
+                                        void* workspace, size_t workspace_bytes, cvh_stream_t stream);
+int cvh_paged_attention_fp8_merge_phase(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                        const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                        int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                                        int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                        int block_size, int scale_mode, double scale, int split_tokens,
+                                        void* workspace, size_t workspace_bytes, cvh_stream_t stream);
+
 /* Workspace bytes needed by the calls above (replaces the per-call at::empty of
  * kernels/paged_attention.cu:415-421, which cannot run under graph capture). */
 size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,

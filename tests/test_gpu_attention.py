@@ -217,3 +217,23 @@ def test_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert np.array_equal(bits(out), eager), f"replay {i} differs from eager"
         _ = run_gpu(b)   # eager work between replays
+
+
+def test_split_and_merge_phases_equal_combined_call():
+    say("split phase + merge phase == combined call")
+    from cppvllm_amd import _lib
+    b = dev(synth(47, [3000, 100, 1400], 16))
+    T, H = b["q"].shape[:2]
+    W = b["block_tables"].shape[1]
+    ws = ops.paged_attention_workspace(T, H, 8, 128, W, 16, 64, DEV)
+    base = run_gpu(b, 64)
+    out = torch.empty_like(b["q"])
+    args = (out.data_ptr(), b["q"].data_ptr(), b["k_cache"].data_ptr(), b["v_cache"].data_ptr(),
+            b["k_scale"].data_ptr(), b["v_scale"].data_ptr(), b["block_tables"].data_ptr(), W,
+            b["token_seq"].data_ptr(), b["token_kv_len"].data_ptr(), T, H, 8, 128, 16, 0, b["scale"], 64,
+            ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    lib = _lib.lib()
+    assert lib.cvh_paged_attention_fp8_split_phase(*args) == 0
+    assert lib.cvh_paged_attention_fp8_merge_phase(*args) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), base)

@@ -12,7 +12,7 @@ from cppvllm_amd import _lib, workloads
 def test_library_exports_every_header_symbol():
     lib = _lib.lib()
     names = _lib.header_symbols()
-    assert len(names) >= 11
+    assert len(names) >= 13
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
