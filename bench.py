@@ -81,7 +81,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--partitions", type=int, default=0, help="work partitions (0 = automatic)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain 1 GiB device-to-device copies (rocprofv3 FETCH/WRITE_SIZE scale)")
     args = ap.parse_args()
@@ -117,14 +117,14 @@ def main():
         else:
             layers.append(tuple(x.clone() for x in (b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"])))
     lib = _lib.lib()
-    ws_bytes = lib.cvh_paged_attention_workspace_bytes(T, H, KV, HD, W, BS, args.split_tokens)
+    ws_bytes = lib.cvh_paged_attention_workspace_bytes(T, H, KV, HD, W, BS, args.partitions)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     out = torch.empty_like(b["q"])
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
     fixed = (out.data_ptr(), b["q"].data_ptr())
     tail = (b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(), b["token_kv_len"].data_ptr(), T, H, KV, HD,
-            BS, _lib.SCALE_PER_TOKEN_HEAD, b["scale"], args.split_tokens, ws.data_ptr(), ws_bytes, sp)
+            BS, _lib.SCALE_PER_TOKEN_HEAD, b["scale"], args.partitions, ws.data_ptr(), ws_bytes, sp)
     layer_ptrs = [tuple(x.data_ptr() for x in lay) for lay in layers]
     # the op = decode kernel (split phase) + split merge (merge phase), launched back to back
     split_fn = lib.cvh_paged_attention_fp8_split_phase
@@ -186,8 +186,8 @@ def main():
             "workload": "BASELINE config 3: 256-seq FP8 paged decode step, 28 layers, distinct per-layer caches",
             "seqs": T, "ctx_sum": int(sum(lens)), "ctx_min": int(min(lens)), "ctx_max": int(max(lens)),
             "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "block_size": BS, "layers": len(layer_ptrs),
-            "scale_mode": "per_token_head", "split_tokens": lib.cvh_paged_attention_split_tokens(T, KV, W, BS)
-            if args.split_tokens == 0 else args.split_tokens,
+            "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, KV, W, BS)
+            if args.partitions == 0 else args.partitions,
             "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -1,51 +1,63 @@
-// FP8-e4m3 paged decode attention for gfx950 (CDNA4), one wavefront per
-// (query token, kv head, split).
+// FP8-e4m3 paged decode attention for gfx950 (CDNA4).
 //
-// Reference semantics: kernels/paged_attention.cu:89-393 (per-token causal length, GQA heads
-// sharing each K/V row, per-(token,head) FP8 scales, online softmax in fp32, split-K partials
-// merged with a log-sum-exp combine). The decomposition here is designed for wave64:
+// Reference semantics: kernels/paged_attention.cu:89-393 — per query token causal length,
+// GQA query heads sharing each K/V row, per-(token, kv head) FP8 scales, online softmax in fp32,
+// split partials merged with a log-sum-exp combine.
 //
-//   * lane = (grp, sub): grp = lane/8 picks one of 8 keys of a step, sub = lane%8 owns a
-//     16-byte (HD=128) or 8-byte (HD=64) slice of the 128-byte K and V rows, so each load
-//     instruction covers 8 full key rows (8 x 128 B cache lines, no partial lines);
-//   * a tile is 4 steps = 32 keys; tile t+1's K/V/scale loads are issued before tile t is
-//     computed (register double buffer) to keep >= 8 KB in flight per wave;
-//   * K/V loads are non-temporal (streamed once), and a workgroup carries the waves of 4
-//     consecutive kv heads of one (token, split) so whole 1 KB slot rows are read together;
+// Work decomposition (persistent, balanced — "stream-K" over the key axis):
+//   * a *row* is (query token t, group of WPG consecutive kv heads); it has
+//     ntiles(t) = ceil(kv_len(t) / 32) tiles of 32 keys. Rows are laid end to end in (t, group)
+//     order, giving U tiles in total. Every workgroup builds the prefix sum of the row tile counts
+//     in LDS from token_kv_len (no host knowledge of the lengths is needed, so the launch is
+//     capture-safe), and processes exactly the tiles [w*U/G, (w+1)*U/G) for its index w of G.
+//     Ragged contexts therefore cost no load imbalance and there is no tail of short items.
+//   * a workgroup has WPG waves, one per kv head of the row group; they walk the same tiles, so
+//     whole 1 KB slot rows (all heads of a token) are read together.
+//   * a row piece that is cut by a workgroup boundary is written as an (acc, max, sum) partial to
+//     one of two per-workgroup slots (0: the piece containing the workgroup's first tile, 1: the
+//     one containing its last); whole rows are finished in place. paged_merge_kernel combines
+//     the pieces of cut rows.
+//
+// Per wave (one kv head, REP query heads), designed for wave64:
+//   * lane = (grp, sub): grp = lane/8 picks one of 8 keys of a step, sub = lane%8 owns a 16-byte
+//     (HD=128) or 8-byte (HD=64) slice of the 128-byte K and V rows, so each load instruction
+//     covers 8 full key rows (8 x 128 B cache lines);
+//   * a tile is 4 steps = 32 keys; the next tile's K/V/scale loads are issued before the current
+//     one is computed (register double buffer, unrolled by two, straight-line prefetch so the wait
+//     before each compute covers only its own tile); block-table lookups run one tile ahead;
+//   * raw buffer loads with the non-temporal hint; a prefetch past the piece's end gets a
+//     zero-size descriptor and returns zeros without memory traffic;
 //   * FP8 -> f32 with the hardware OCP converter (v_cvt_pk_f32_fp8, exact for finite codes);
 //   * q.k partial dots reduce over the 8 lanes of a key with DPP (quad_perm, half-mirror);
-//   * softmax in base 2 (scale*log2(e) folded into q) with a lazy running max: the
-//     accumulator is only rescaled when a tile's max exceeds the running max by 8 (p <= 256),
-//     which is exact because the final normalisation uses the same max for l and acc;
-//   * the running max is wave-uniform, so the cross-key-group combine at the end is a plain
-//     sum (no per-group rescale);
-//   * split-K: each token's context is cut into chunks of split_tiles*32 keys; a token with one
-//     chunk writes bf16 directly, others write (acc, m, l) partials for the merge kernel.
+//   * softmax in base 2 (scale*log2(e) folded into q) with a running max per key group and a
+//     lazy rescale (only when a tile's max exceeds the running max by 2^8), exact because l and
+//     acc share the stale max; groups are combined once per piece (DPP row_ror:8, permlane swaps).
 #include <hip/hip_runtime.h>
 
 #include <math.h>
 
 #include <algorithm>
-#include <type_traits>
 
 #include "cvh_device.h"
 
 namespace cvh {
 namespace {
 
-constexpr int kTileKeys = 32;      // keys per wave per tile (4 steps x 8 key groups)
-constexpr int kSteps = 4;
+constexpr int kSteps = 4;                  // 8-key steps per tile
+constexpr int kTileKeys = 8 * kSteps;      // 32 keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleThreshold = 8.0f;   // log2 units: stale max tolerated up to p = 2^8
+constexpr float kRescaleThreshold = 8.0f;  // log2 units: stale max tolerated up to p = 2^8
 constexpr float kMinusHuge = -1e30f;
+constexpr int kMaxRows = 16383;            // rows (tokens x head groups) per launch: LDS prefix
+constexpr int kAutoPartitions = 512;       // MI355X: 256 CUs x 2 resident 4-wave workgroups
 
+// ---- buffer loads ------------------------------------------------------------------------------
 // K/V rows and scales go through raw buffer loads: the descriptor's record count bounds every
-// access, so a tile that must not be read (the prefetch issued past a split's last tile) is given
-// a zero-size descriptor and returns zeros without touching memory. All K/V/scale loads carry the
-// non-temporal hint: each byte is read once per launch, so it should not displace reusable lines
-// (block tables, q, partials) in L2 / MALL (measured: -8% kernel time at config 3).
-constexpr int kBufferWord3 = 0x00020000;      // raw buffer, 32-bit data format (gfx9 encoding)
-constexpr int kNonTemporal = 2;               // cache-policy bits of the load: nt
+// access, so a tile that must not be read is given a zero-size descriptor and returns zeros
+// without touching memory. All K/V/scale loads carry the non-temporal hint: each byte is read
+// once per launch and should not displace reusable lines (block tables, q, partials).
+constexpr int kBufferWord3 = 0x00020000;   // raw buffer, 32-bit data format (gfx9 encoding)
+constexpr int kNonTemporal = 2;            // cache-policy bits of the load: nt
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -84,6 +96,7 @@ template <> struct KvVec<64> {
     }
 };
 
+// ---- cross-lane reductions ------------------------------------------------------------------------
 // Sum over the 8 lanes of a key group (lanes 8k..8k+7); result in every lane of the group.
 __device__ __forceinline__ float group8_sum(float v) {
     v = v + dpp_xor1(v);
@@ -91,9 +104,9 @@ __device__ __forceinline__ float group8_sum(float v) {
     v = v + dpp_half_mirror(v);
     return v;
 }
-// Exchange across rows of 16 / halves of 32 lanes with the gfx950 permlane swaps (no LDS, no
-// LGKM counter traffic): with both operands = v, the pair returned holds, per lane, its own
-// value and its xor-16 (resp. xor-32) partner's value.
+// Exchange across rows of 16 / halves of 32 lanes with the gfx950 permlane swaps (no LDS): with
+// both operands = v, the returned pair holds, per lane, its own value and its xor-16 (resp.
+// xor-32) partner's value.
 __device__ __forceinline__ float xor16_sum(float v) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -110,75 +123,76 @@ __device__ __forceinline__ float xor32_max(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-// Combine the 8 key groups (sum), result in every lane; lanes with equal sub get equal values.
+// Sum over the 8 key groups; lanes with equal sub end with equal values.
 __device__ __forceinline__ float across_groups_sum(float v) {
     v = v + dpp_xor8(v);
     v = xor16_sum(v);
     return xor32_sum(v);
 }
-// Max over the whole wave of a value that is already uniform inside each key group.
+// Max over the whole wave of a value that is uniform inside each key group.
 __device__ __forceinline__ float across_groups_max(float v) {
     v = fmaxf(v, dpp_xor8(v));
     v = xor16_max(v);
     return xor32_max(v);
 }
 
-// ONE_BLOCK: block_size >= 32, so a 32-key tile never straddles two cache blocks and one
-// block-table lookup serves the whole tile. Otherwise (block_size 16) each 8-key step still lies
-// in a single block, looked up per step. Lookups are wave-uniform scalar loads; the per-lane
-// address is a 32-bit offset from a scalar block base.
+struct Params {
+    uint16_t* out;
+    float* part_acc;         // [G][2][WPG][REP][HD]
+    float* part_ml;          // [G][2][WPG][REP][2]
+    int* prefix_out;         // [rows + 1] row tile prefix, written by workgroup 0 for the merge
+    const uint16_t* q;
+    const uint8_t* k_cache;
+    const uint8_t* v_cache;
+    const float* k_scale;
+    const float* v_scale;
+    const int64_t* block_tables;
+    int64_t table_width;
+    const int64_t* token_seq;
+    const int64_t* token_kv_len;
+    int num_tokens;
+    int n_kv;
+    int wpg;                 // kv heads (waves) per workgroup
+    int log2_bs;
+    float q_scale;           // softmax scale * log2(e)
+};
+
+// Causal length of token t, clamped to what its block-table row can address.
+__device__ __forceinline__ int token_len(const Params& p, int t) {
+    int64_t kv = p.token_kv_len[t];
+    const int64_t cap = p.table_width << p.log2_bs;
+    if (kv > cap) kv = cap;
+    return kv > 0 ? static_cast<int>(kv) : 0;
+}
+
+// Attention of one wave (kv head g, REP query heads of token t) over tiles [tb, te) of the
+// token's context. Returns the piece's wave max m, sum l and unnormalised acc (valid in all
+// lanes; lane `sub` holds dims sub*E .. sub*E+E-1).
 template <int HD, int REP, int SM, bool ONE_BLOCK>
-__global__ __launch_bounds__(256) void paged_decode_kernel(
-        uint16_t* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
-        const uint16_t* __restrict__ q, const uint8_t* __restrict__ k_cache, const uint8_t* __restrict__ v_cache,
-        const float* __restrict__ k_scale, const float* __restrict__ v_scale, const int64_t* __restrict__ block_tables,
-        int64_t table_width, const int64_t* __restrict__ token_seq, const int64_t* __restrict__ token_kv_len,
-        int n_kv, int log2_bs, int split_tiles, int max_splits, float q_scale) {
+__device__ __forceinline__ void scan_tiles(const Params& p, int t, int g, int kv_len, int tb, int te, float (&m)[REP],
+                                           float (&l)[REP], float (&acc)[REP][KvVec<HD>::kElems]) {
     using V = KvVec<HD>;
     using VT = typename V::T;
-    constexpr int E = V::kElems;                 // elements of HD owned per lane
-    // A workgroup holds the waves of (blockDim.x/64) consecutive kv heads of one (token, split):
-    // together they read whole slot rows, so the HBM pages they touch are read at the same time.
-    const int t = blockIdx.x;
-    // wave-uniform by construction; readfirstlane tells the compiler so (scalar descriptors)
-    const int g = __builtin_amdgcn_readfirstlane(blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6));
-    const int split = blockIdx.z;
+    constexpr int E = V::kElems;
     const int lane = threadIdx.x & 63;
     const int grp = lane >> 3;
     const int sub = lane & 7;
-    const int H = n_kv * REP;
-
-    int64_t kv64 = token_kv_len[t];
-    const int64_t cap = table_width << log2_bs;  // never read past the block table row
-    if (kv64 > cap) kv64 = cap;
-    if (kv64 <= 0) {                             // empty context: zero output (reference: 0/0)
-        if (split == 0) {
-#pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                uint16_t* o = out + ((int64_t)t * H + g * REP + r) * HD;
-                for (int d = lane; d < HD; d += 64) o[d] = 0;
-            }
-        }
-        return;
-    }
-    const int kv_len = static_cast<int>(kv64);   // the host limits table_width*block_size < 2^31
-    const int ntiles = (kv_len + kTileKeys - 1) / kTileKeys;
-    const int nsplit = (ntiles + split_tiles - 1) / split_tiles;
-    if (split >= nsplit) return;
-    const int tile_begin = split * split_tiles;
-    const int tile_end = min(ntiles, tile_begin + split_tiles);
-    const int64_t* table = block_tables + token_seq[t] * table_width;
-    const uint32_t row_bytes = static_cast<uint32_t>(n_kv) * HD;    // bytes of one slot (all kv heads)
+    const int H = p.n_kv * REP;
+    const int log2_bs = p.log2_bs;
+    const int64_t* table = p.block_tables + p.token_seq[t] * p.table_width;
+    const uint32_t row_bytes = static_cast<uint32_t>(p.n_kv) * HD;   // bytes of one slot (all kv heads)
     const int64_t blk_bytes = static_cast<int64_t>(row_bytes) << log2_bs;
+    const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
+    const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
     const int bs_mask = (1 << log2_bs) - 1;
-    const uint32_t lane_col = g * HD + sub * E;  // byte column of this lane inside a slot row
+    const uint32_t lane_col = g * HD + sub * E;                     // byte column inside a slot row
 
-    // ---- q slice for the REP heads of this kv head, pre-scaled by scale*log2(e) [*k_scale]
-    const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? q_scale * k_scale[0] : q_scale;
+    // q slice for the REP heads of this kv head, pre-scaled by scale*log2(e) [*k_scale]
+    const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? p.q_scale * p.k_scale[0] : p.q_scale;
     float qf[REP][E];
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-        const uint16_t* qr = q + ((int64_t)t * H + g * REP + r) * HD + sub * E;
+        const uint16_t* qr = p.q + ((int64_t)t * H + g * REP + r) * HD + sub * E;
 #pragma unroll
         for (int c = 0; c < E / 8; ++c) {
             const uint4 u = reinterpret_cast<const uint4*>(qr)[c];
@@ -190,10 +204,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
             }
         }
     }
-
-    // Running max per key group (lanes 8k..8k+7 agree on it): no cross-group exchange per tile.
-    // Starts at a finite floor so that a group whose keys are all masked gives exp2(-inf) = 0.
-    float m[REP], l[REP], acc[REP][E];
+    // running max per key group; a finite floor so an all-masked group gives exp2(-inf) = 0
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
         m[r] = kMinusHuge;
@@ -202,56 +213,47 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
         for (int e = 0; e < E; ++e) acc[r][e] = 0.f;
     }
 
-    // ---- tile loader: K/V slices and per-key scales for keys tile*32 + 8*s + grp.
-    // Keys past kv_len (last tile only) are clamped to key kv_len-1: a valid, finite row whose
-    // score is masked, so no garbage (possibly NaN) cache byte ever reaches the accumulator.
     struct Tile {
         VT k[kSteps], v[kSteps];
         float ks[kSteps], vs[kSteps];
     };
     // Physical blocks of a tile: `lo` for its first 16 keys, `hi` for the last 16 (equal unless
-    // block_size == 16). Both wave-uniform (scalar loads); looked up one tile ahead of use.
+    // block_size == 16). Wave-uniform scalar loads, looked up one tile ahead of use.
     struct Phys {
         int64_t lo, hi;
     };
     auto lookup = [&](int tile) -> Phys {
-        tile = min(tile, tile_end - 1);
+        tile = min(tile, te - 1);
         const int p0 = tile * kTileKeys;
         const int64_t lo = max(table[p0 >> log2_bs], int64_t{0});
         if constexpr (ONE_BLOCK) return {lo, lo};
-        const int64_t hi = max(table[min(p0 + 16, kv_len - 1) >> log2_bs], int64_t{0});
+        const int64_t hi = max(table[min(p0 + kTileKeys / 2, kv_len - 1) >> log2_bs], int64_t{0});
         return {lo, hi};
     };
-    // live = false: the prefetch past the split's last tile; zero-size descriptors, no traffic.
-    const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
-    const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
+    // Keys past kv_len (last tile only) are clamped to key kv_len-1: a valid, finite row whose
+    // score is masked. live = false: the prefetch past the piece's end (zero-size descriptors).
     auto load_tile = [&](int tile, Tile& tl, Phys ph2, bool live) {
         const int p0 = tile * kTileKeys;
-        const uint32_t lv = static_cast<uint32_t>(live);               // arithmetic, not a branch
+        const uint32_t lv = static_cast<uint32_t>(live);            // arithmetic, not a branch
         const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
-            const int64_t ph = (ONE_BLOCK || s < 2) ? ph2.lo : ph2.hi;
+            const int64_t ph = (ONE_BLOCK || s < kSteps / 2) ? ph2.lo : ph2.hi;
             const int pos = min(p0 + 8 * s + grp, kv_len - 1);
             const uint32_t in_blk = static_cast<uint32_t>(pos & bs_mask);
             const uint32_t off = in_blk * row_bytes + lane_col;
-            const __amdgpu_buffer_rsrc_t kr = make_rsrc(k_cache + ph * blk_bytes, kv_rec);
-            const __amdgpu_buffer_rsrc_t vr = make_rsrc(v_cache + ph * blk_bytes, kv_rec);
-            tl.k[s] = buf_load<VT>(kr, off);
-            tl.v[s] = buf_load<VT>(vr, off);
+            tl.k[s] = buf_load<VT>(make_rsrc(p.k_cache + ph * blk_bytes, kv_rec), off);
+            tl.v[s] = buf_load<VT>(make_rsrc(p.v_cache + ph * blk_bytes, kv_rec), off);
             if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
-                const int64_t sbase = (ph * n_kv + g) << log2_bs;
-                const __amdgpu_buffer_rsrc_t ksr = make_rsrc(k_scale + sbase, s_rec);
-                const __amdgpu_buffer_rsrc_t vsr = make_rsrc(v_scale + sbase, s_rec);
-                tl.ks[s] = buf_load_f32(ksr, in_blk * 4u);
-                tl.vs[s] = buf_load_f32(vsr, in_blk * 4u);
+                const int64_t sbase = (ph * p.n_kv + g) << log2_bs;
+                tl.ks[s] = buf_load_f32(make_rsrc(p.k_scale + sbase, s_rec), in_blk * 4u);
+                tl.vs[s] = buf_load_f32(make_rsrc(p.v_scale + sbase, s_rec), in_blk * 4u);
             } else {
                 tl.ks[s] = 1.f;
                 tl.vs[s] = 1.f;
             }
         }
     };
-
     auto compute = [&](int tile, const Tile& tl) {
         const int p0 = tile * kTileKeys;
         float sc[REP][kSteps];
@@ -279,7 +281,9 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-            const float mt = fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3]));
+            float mt = sc[r][0];
+#pragma unroll
+            for (int s = 1; s < kSteps; ++s) mt = fmaxf(mt, sc[r][s]);
             const bool need = mt > m[r] + kRescaleThreshold;    // per key group
             if (__builtin_amdgcn_ballot_w64(need) != 0) {      // wave-uniform; rare after tile 0
                 const float mn = need ? mt : m[r];
@@ -291,10 +295,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
             }
 #pragma unroll
             for (int s = 0; s < kSteps; ++s) {
-                const float p = __builtin_amdgcn_exp2f(sc[r][s] - m[r]);
-                l[r] += p;
-                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) sc[r][s] = p * tl.vs[s];
-                else sc[r][s] = p;
+                const float pr = __builtin_amdgcn_exp2f(sc[r][s] - m[r]);
+                l[r] += pr;
+                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) sc[r][s] = pr * tl.vs[s];
+                else sc[r][s] = pr;
             }
         }
 #pragma unroll
@@ -310,107 +314,211 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
         }
     };
 
-    // Register double buffer, unrolled by two so no tile is ever copied between buffers; the
-    // block-table lookup runs one tile ahead of the loads that use it. The prefetch is issued
-    // unconditionally (past the end with zero-size descriptors) so that it sits in straight-line
-    // code and the wait before each compute only covers the tile it consumes.
-    Tile ta, tb;
-    Phys pa_ = lookup(tile_begin);
-    Phys pb_ = lookup(tile_begin + 1);
-    load_tile(tile_begin, ta, pa_, true);
-    for (int tile = tile_begin;; tile += 2) {
-        load_tile(min(tile + 1, tile_end - 1), tb, pb_, tile + 1 < tile_end);
-        pa_ = lookup(tile + 2);
+    Tile ta, tbuf;
+    Phys pa = lookup(tb);
+    Phys pb = lookup(tb + 1);
+    load_tile(tb, ta, pa, true);
+    for (int tile = tb;; tile += 2) {
+        load_tile(min(tile + 1, te - 1), tbuf, pb, tile + 1 < te);
+        pa = lookup(tile + 2);
         compute(tile, ta);
-        if (tile + 1 >= tile_end) break;
-        load_tile(min(tile + 2, tile_end - 1), ta, pa_, tile + 2 < tile_end);
-        pb_ = lookup(tile + 3);
-        compute(tile + 1, tb);
-        if (tile + 2 >= tile_end) break;
+        if (tile + 1 >= te) break;
+        load_tile(min(tile + 2, te - 1), ta, pa, tile + 2 < te);
+        pb = lookup(tile + 3);
+        compute(tile + 1, tbuf);
+        if (tile + 2 >= te) break;
     }
 
-    // ---- combine the 8 key groups: rescale each to the wave max, then sum
+    // combine the 8 key groups: rescale each to the wave max, then sum
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
         const float M = across_groups_max(m[r]);
         const float c = __builtin_amdgcn_exp2f(m[r] - M);
         m[r] = M;
-        // l is uniform inside a group (every lane of a group sums the same p's); sum over groups.
-        l[r] = across_groups_sum(l[r] * c);
+        l[r] = across_groups_sum(l[r] * c);   // l is uniform inside a group
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[r][e] = across_groups_sum(acc[r][e] * c);
     }
-    if (grp != 0) return;
+}
 
-    const float v_fin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
+// Exclusive prefix of row tile counts into LDS (prefix[0..rows]); all threads of the block.
+__device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int hg_count, int* prefix) {
+    __shared__ int wave_tot[16];
+    const int nthreads = blockDim.x;
+    const int tid = threadIdx.x;
+    const int per = (rows + nthreads - 1) / nthreads;
+    const int beg = min(rows, tid * per), end = min(rows, beg + per);
+    int s = 0;
+    for (int r = beg; r < end; ++r) s += (token_len(p, r / hg_count) + kTileKeys - 1) / kTileKeys;
+    // inclusive scan over the wave
+    const int lane = tid & 63, wv = tid >> 6;
+    int incl = s;
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        const int64_t head = (int64_t)t * H + g * REP + r;
-        if (nsplit == 1) {
-            const float f = v_fin / l[r];
-            uint16_t* o = out + head * HD + sub * E;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wave_tot[wv] = incl;
+    __syncthreads();
+    int off = 0;
+    for (int i = 0; i < wv; ++i) off += wave_tot[i];
+    int run = off + incl - s;            // exclusive prefix of this thread's chunk
+    for (int r = beg; r < end; ++r) {
+        prefix[r] = run;
+        run += (token_len(p, r / hg_count) + kTileKeys - 1) / kTileKeys;
+    }
+    if (tid == nthreads - 1) {
+        int tot = 0;
+        for (int i = 0; i < nthreads / 64; ++i) tot += wave_tot[i];
+        prefix[rows] = tot;
+    }
+    __syncthreads();
+}
+
+template <int HD, int REP, int SM, bool ONE_BLOCK>
+__global__ __launch_bounds__(256) void paged_decode_kernel(Params p) {
+    using V = KvVec<HD>;
+    constexpr int E = V::kElems;
+    extern __shared__ int prefix[];
+    const int wpg = p.wpg;
+    const int hg_count = p.n_kv / wpg;
+    const int rows = p.num_tokens * hg_count;
+    build_row_prefix(p, rows, hg_count, prefix);
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
+
+    const int64_t U = prefix[rows];
+    const int64_t G = gridDim.x;
+    const int w = blockIdx.x;
+    const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
+    const bool last_wg = (w == G - 1);
+    const int lane = threadIdx.x & 63;
+    const int sub = lane & 7;
+    const int grp = lane >> 3;
+    // wave-uniform by construction; readfirstlane tells the compiler so (scalar descriptors)
+    const int wi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = p.n_kv * REP;
+
+    // first row to visit: the row holding tile u0, or the first of the empty rows sitting at u0
+    int lo = 0, hi = rows;               // last r with prefix[r] <= u0
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (prefix[mid] <= u0) lo = mid;
+        else hi = mid;
+    }
+    int r = lo;
+    if (prefix[r] == u0) {               // rewind over empty rows that also start at u0
+        int a = 0, b = r;
+        while (a < b) {
+            const int mid = (a + b) >> 1;
+            if (prefix[mid] < u0) a = mid + 1;
+            else b = mid;
+        }
+        r = a;
+    }
+    for (; r < rows; ++r) {
+        const int64_t pr0 = prefix[r], pr1 = prefix[r + 1];
+        if (!(pr0 < u1 || (last_wg && pr0 == U))) break;
+        const int t = r / hg_count;
+        const int g = (r % hg_count) * wpg + wi;
+        if (pr1 == pr0) {                // empty context: zero output (reference: 0/0)
 #pragma unroll
-            for (int c = 0; c < E / 8; ++c) {
-                uint32_t w[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    w[i] = f32_to_bf16_bits(acc[r][c * 8 + 2 * i] * f) |
-                           (uint32_t(f32_to_bf16_bits(acc[r][c * 8 + 2 * i + 1] * f)) << 16);
-                }
-                reinterpret_cast<uint4*>(o)[c] = make_uint4(w[0], w[1], w[2], w[3]);
+            for (int rr = 0; rr < REP; ++rr) {
+                uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD;
+                for (int d = lane; d < HD; d += 64) o[d] = 0;
             }
-        } else {
-            const int64_t slot = head * max_splits + split;
-            float* pa = part_acc + slot * HD + sub * E;
+            continue;
+        }
+        const int tb = static_cast<int>(max(u0, pr0) - pr0);
+        const int te = static_cast<int>(min(u1, pr1) - pr0);
+        if (tb >= te) continue;
+        float m[REP], l[REP], acc[REP][E];
+        scan_tiles<HD, REP, SM, ONE_BLOCK>(p, t, g, token_len(p, t), tb, te, m, l, acc);
+        if (grp != 0) continue;
+        if (tb == 0 && te == pr1 - pr0) {  // whole row: finish in place
+            const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
 #pragma unroll
-            for (int c = 0; c < E / 4; ++c)
-                reinterpret_cast<float4*>(pa)[c] =
-                        make_float4(acc[r][4 * c], acc[r][4 * c + 1], acc[r][4 * c + 2], acc[r][4 * c + 3]);
-            if (sub == 0) reinterpret_cast<float2*>(part_ml)[slot] = make_float2(m[r], l[r]);
+            for (int rr = 0; rr < REP; ++rr) {
+                const float f = vfin / l[rr];
+                uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD + sub * E;
+#pragma unroll
+                for (int c = 0; c < E / 8; ++c) {
+                    uint32_t wd[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        wd[i] = f32_to_bf16_bits(acc[rr][c * 8 + 2 * i] * f) |
+                                (uint32_t(f32_to_bf16_bits(acc[rr][c * 8 + 2 * i + 1] * f)) << 16);
+                    reinterpret_cast<uint4*>(o)[c] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                }
+            }
+        } else {                          // cut row: partial to slot 0 (holds u0) or 1 (holds u1-1)
+            const int slot = (pr0 <= u0) ? 0 : 1;
+#pragma unroll
+            for (int rr = 0; rr < REP; ++rr) {
+                const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP + rr;
+                float* pa = p.part_acc + idx * HD + sub * E;
+#pragma unroll
+                for (int c = 0; c < E / 4; ++c)
+                    reinterpret_cast<float4*>(pa)[c] =
+                            make_float4(acc[rr][4 * c], acc[rr][4 * c + 1], acc[rr][4 * c + 2], acc[rr][4 * c + 3]);
+                if (sub == 0) reinterpret_cast<float2*>(p.part_ml)[idx] = make_float2(m[rr], l[rr]);
+            }
         }
     }
 }
 
-// Log-sum-exp merge of the split partials (reference: kernels/paged_attention.cu:361-393).
-// One wave per (token, head); lane d handles dims d and d+64.
+// Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One wave per
+// (token, query head); it recomputes which workgroups covered the row from the prefix the decode
+// kernel stored, and exits for rows finished in place.
 template <int HD, int SM>
 __global__ __launch_bounds__(64) void paged_merge_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
                                                          const float* __restrict__ part_ml,
-                                                         const int64_t* __restrict__ token_kv_len,
-                                                         const float* __restrict__ v_scale, int64_t table_width,
-                                                         int log2_bs, int n_heads, int split_tiles, int max_splits) {
+                                                         const int* __restrict__ prefix,
+                                                         const float* __restrict__ v_scale, int num_tokens, int n_kv,
+                                                         int rep, int wpg, int G) {
     const int h = blockIdx.x;
     const int t = blockIdx.y;
-    int64_t kv_len = token_kv_len[t];
-    const int64_t cap = table_width << log2_bs;
-    if (kv_len > cap) kv_len = cap;
-    if (kv_len <= 0) return;
-    const int64_t ntiles = (kv_len + kTileKeys - 1) / kTileKeys;
-    const int nsplit = static_cast<int>((ntiles + split_tiles - 1) / split_tiles);
-    if (nsplit <= 1) return;
-    const int64_t head = (int64_t)t * n_heads + h;
-    const float2* ml = reinterpret_cast<const float2*>(part_ml) + head * max_splits;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[s].x);
-    float L = 0.f;
+    const int g = h / rep, rr = h % rep;
+    const int hg_count = n_kv / wpg;
+    const int row = t * hg_count + g / wpg, wi = g % wpg;
+    const int rows = num_tokens * hg_count;
+    const int64_t U = prefix[rows];
+    const int64_t pr0 = prefix[row], pr1 = prefix[row + 1];
+    if (pr1 == pr0) return;
+    // workgroup holding tile u: the largest w with w*U/G <= u
+    auto owner = [&](int64_t u) { return static_cast<int>(((u + 1) * G - 1) / U); };
+    const int w0 = owner(pr0), w1 = owner(pr1 - 1);
+    if (w0 == w1) return;
+    // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
+    float M = kMinusHuge;
+    for (int w = w0; w <= w1; ++w) {
+        if (w * U / G == (w + 1) * U / G) continue;
+        const int slot = (pr0 <= w * U / G) ? 0 : 1;
+        const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * rep + rr;
+        M = fmaxf(M, reinterpret_cast<const float2*>(part_ml)[idx].x);
+    }
     constexpr int PER = HD / 64;
-    float A[PER];
+    float L = 0.f, A[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) A[i] = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-        const float2 v = ml[s];
-        const float c = exp2f(v.x - M);
-        L += v.y * c;
-        const float* pa = part_acc + (head * max_splits + s) * HD;
+    for (int w = w0; w <= w1; ++w) {
+        if (w * U / G == (w + 1) * U / G) continue;
+        const int slot = (pr0 <= w * U / G) ? 0 : 1;
+        const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * rep + rr;
+        const float2 ml = reinterpret_cast<const float2*>(part_ml)[idx];
+        const float c = exp2f(ml.x - M);
+        L += ml.y * c;
+        const float* pa = part_acc + idx * HD;
 #pragma unroll
         for (int i = 0; i < PER; ++i) A[i] += pa[threadIdx.x + 64 * i] * c;
     }
     const float f = ((SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f) / L;
-    uint16_t* o = out + head * HD;
+    uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD;
 #pragma unroll
     for (int i = 0; i < PER; ++i) o[threadIdx.x + 64 * i] = f32_to_bf16_bits(A[i] * f);
 }
 
+// ---- host side ------------------------------------------------------------------------------------
 int ilog2_pow2(int64_t v) {
     if (v <= 0 || (v & (v - 1)) != 0) return -1;
     int l = 0;
@@ -418,85 +526,65 @@ int ilog2_pow2(int64_t v) {
     return l;
 }
 
-int64_t max_context(int64_t table_width, int block_size) { return table_width * block_size; }
+int waves_per_group(int n_kv) { return (n_kv % 4 == 0) ? 4 : (n_kv % 2 == 0) ? 2 : 1; }
 
-int auto_split_tokens(int64_t num_tokens, int n_kv, int64_t table_width, int block_size) {
-    // Aim for >= 2048 waves (8 per CU on 256 CUs) when the longest possible context allows it,
-    // with chunks no shorter than 64 keys; 512-key chunks otherwise (64 KB of K+V per wave).
-    const int64_t ctx = std::max<int64_t>(1, max_context(table_width, block_size));
-    int chunk = 512;
-    while (chunk > 64 && num_tokens * n_kv * ((ctx + chunk - 1) / chunk) < 2048) chunk >>= 1;
-    return chunk;
+// Upper bound of the tile count U, from what the host knows (widths, not lengths).
+int64_t tile_bound(int64_t T, int n_kv, int64_t table_width, int block_size) {
+    const int64_t per_row = (table_width * block_size + kTileKeys - 1) / kTileKeys;
+    return T * (n_kv / waves_per_group(n_kv)) * per_row;
 }
 
-bool valid_split(int split_tokens) { return split_tokens >= 64 && split_tokens % kTileKeys == 0; }
-
-int64_t num_splits_max(int64_t table_width, int block_size, int split_tokens) {
-    const int64_t ctx = max_context(table_width, block_size);
-    return std::max<int64_t>(1, (ctx + split_tokens - 1) / split_tokens);
+int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
+    // one partition per resident workgroup slot, but never less than 2 tiles per partition
+    const int64_t b = (tile_bound(T, n_kv, table_width, block_size) + 1) / 2;
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kAutoPartitions, b)));
 }
 
-size_t ws_bytes(int64_t T, int H, int HD, int64_t splits) {
-    if (splits <= 1) return 0;
-    return static_cast<size_t>(T) * H * splits * (HD + 2) * sizeof(float);
+// Workspace: prefix int32 [rows + 1] | part_acc float [G][2][WPG][REP][HD] | part_ml float2 [...]
+struct Workspace {
+    size_t prefix_off, acc_off, ml_off, total;
+};
+size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
+Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
+    const int64_t hg = n_kv / waves_per_group(n_kv);
+    const int64_t rows = T * hg;
+    const int64_t slots = static_cast<int64_t>(G) * 2 * (n_heads / hg);   // [G][2][WPG*REP]
+    Workspace w;
+    w.prefix_off = 0;
+    w.acc_off = align256(static_cast<size_t>(rows + 1) * sizeof(int));
+    w.ml_off = w.acc_off + align256(static_cast<size_t>(slots) * HD * sizeof(float));
+    w.total = w.ml_off + align256(static_cast<size_t>(slots) * 2 * sizeof(float));
+    return w;
 }
+
+enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3 };
 
 template <int HD, int REP, int SM>
-void launch(dim3 grid, int threads, hipStream_t s, void* out, float* pa, float* pm, const void* q, const uint8_t* kc,
-            const uint8_t* vc, const float* ks, const float* vs, const int64_t* bt, int64_t tw, const int64_t* ts,
-            const int64_t* tl, int n_kv, int lg, int split_tiles, int max_splits, float qs) {
-    if (lg >= 5)
-        paged_decode_kernel<HD, REP, SM, true><<<grid, threads, 0, s>>>(static_cast<uint16_t*>(out), pa, pm,
-                                                                   static_cast<const uint16_t*>(q), kc, vc, ks, vs, bt,
-                                                                   tw, ts, tl, n_kv, lg, split_tiles, max_splits, qs);
+void launch_decode(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
+    if (one_block)
+        paged_decode_kernel<HD, REP, SM, true><<<dim3(G), threads, lds, s>>>(p);
     else
-        paged_decode_kernel<HD, REP, SM, false><<<grid, threads, 0, s>>>(static_cast<uint16_t*>(out), pa, pm,
-                                                                    static_cast<const uint16_t*>(q), kc, vc, ks, vs,
-                                                                    bt, tw, ts, tl, n_kv, lg, split_tiles, max_splits,
-                                                                    qs);
+        paged_decode_kernel<HD, REP, SM, false><<<dim3(G), threads, lds, s>>>(p);
 }
 
 template <int HD, int SM>
-bool launch_rep(int rep, dim3 grid, int threads, hipStream_t s, void* out, float* pa, float* pm, const void* q,
-                const uint8_t* kc, const uint8_t* vc, const float* ks, const float* vs, const int64_t* bt, int64_t tw,
-                const int64_t* ts, const int64_t* tl, int n_kv, int lg, int st, int ms, float qs) {
+bool launch_decode_rep(int rep, int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
     switch (rep) {
-        case 1: launch<HD, 1, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
-        case 2: launch<HD, 2, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
-        case 4: launch<HD, 4, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
-        case 8: launch<HD, 8, SM>(grid, threads, s, out, pa, pm, q, kc, vc, ks, vs, bt, tw, ts, tl, n_kv, lg, st, ms, qs); return true;
+        case 1: launch_decode<HD, 1, SM>(G, threads, lds, s, p, one_block); return true;
+        case 2: launch_decode<HD, 2, SM>(G, threads, lds, s, p, one_block); return true;
+        case 4: launch_decode<HD, 4, SM>(G, threads, lds, s, p, one_block); return true;
+        case 8: launch_decode<HD, 8, SM>(G, threads, lds, s, p, one_block); return true;
         default: return false;
     }
 }
 
-}  // namespace
-}  // namespace cvh
-
-extern "C" int cvh_paged_attention_split_tokens(int64_t num_tokens, int n_kv_heads, int64_t table_width,
-                                                int block_size) {
-    if (num_tokens <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0) return 512;
-    return cvh::auto_split_tokens(num_tokens, n_kv_heads, table_width, block_size);
-}
-
-extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                                                      int64_t table_width, int block_size, int split_tokens) {
-    if (num_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0) return 0;
-    if (split_tokens == 0) split_tokens = cvh::auto_split_tokens(num_tokens, n_kv_heads, table_width, block_size);
-    if (!cvh::valid_split(split_tokens)) return 0;
-    return cvh::ws_bytes(num_tokens, n_heads, head_dim,
-                                cvh::num_splits_max(table_width, block_size, split_tokens));
-}
-
-namespace cvh {
-namespace {
-enum Phase { kPhaseSplit = 1, kPhaseMerge = 2, kPhaseBoth = 3 };
-
 int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache, const float* k_scale,
                     const float* v_scale, const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
                     const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                    int block_size, int scale_mode, double scale, int split_tokens, void* workspace,
+                    int block_size, int scale_mode, double scale, int partitions, void* workspace,
                     size_t workspace_bytes, cvh_stream_t stream, int phase) {
-    if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0) return CVH_ERR_INVALID_ARG;
+    if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0 || partitions < 0)
+        return CVH_ERR_INVALID_ARG;
     if (num_tokens == 0) return CVH_OK;
     if (!out || !q || !k_cache || !v_cache || !k_scale || !v_scale || !block_tables || !token_seq || !token_kv_len)
         return CVH_ERR_INVALID_ARG;
@@ -508,86 +596,111 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (lg < 4 || lg > 12) return CVH_ERR_UNSUPPORTED;
     if (head_dim != 64 && head_dim != 128) return CVH_ERR_UNSUPPORTED;
     if (scale_mode != CVH_SCALE_PER_TOKEN_HEAD && scale_mode != CVH_SCALE_PER_TENSOR) return CVH_ERR_UNSUPPORTED;
-    if (num_tokens > 0x7fffffff || n_kv_heads > 65535) return CVH_ERR_UNSUPPORTED;
-    if (split_tokens == 0) split_tokens = auto_split_tokens(num_tokens, n_kv_heads, table_width, block_size);
-    if (!valid_split(split_tokens)) return CVH_ERR_INVALID_ARG;
-    const int64_t ms = num_splits_max(table_width, block_size, split_tokens);
-    if (ms > 65535) return CVH_ERR_UNSUPPORTED;
     if (table_width > (int64_t{0x7fffffff} >> lg)) return CVH_ERR_UNSUPPORTED;   // contexts < 2^31 keys
-    const size_t need = ws_bytes(num_tokens, n_heads, head_dim, ms);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return CVH_ERR_WORKSPACE;
-    float* pa = static_cast<float*>(workspace);
-    float* pm = need > 0 ? pa + static_cast<size_t>(num_tokens) * n_heads * ms * head_dim : nullptr;
+    const int wpg = waves_per_group(n_kv_heads);
+    const int64_t rows = num_tokens * (n_kv_heads / wpg);
+    if (rows > kMaxRows) return CVH_ERR_UNSUPPORTED;
+    if (tile_bound(num_tokens, n_kv_heads, table_width, block_size) >= (int64_t{1} << 31) / 2)
+        return CVH_ERR_UNSUPPORTED;
+    const int G = partitions ? partitions : auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
+    const Workspace wl = ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G);
+    if (workspace == nullptr || workspace_bytes < wl.total) return CVH_ERR_WORKSPACE;
+    char* wsb = static_cast<char*>(workspace);
 
+    Params p;
+    p.out = static_cast<uint16_t*>(out);
+    p.prefix_out = reinterpret_cast<int*>(wsb + wl.prefix_off);
+    p.part_acc = reinterpret_cast<float*>(wsb + wl.acc_off);
+    p.part_ml = reinterpret_cast<float*>(wsb + wl.ml_off);
+    p.q = static_cast<const uint16_t*>(q);
+    p.k_cache = k_cache;
+    p.v_cache = v_cache;
+    p.k_scale = k_scale;
+    p.v_scale = v_scale;
+    p.block_tables = block_tables;
+    p.table_width = table_width;
+    p.token_seq = token_seq;
+    p.token_kv_len = token_kv_len;
+    p.num_tokens = static_cast<int>(num_tokens);
+    p.n_kv = n_kv_heads;
+    p.wpg = wpg;
+    p.log2_bs = lg;
     // The softmax scale is folded into q with log2(e) (base-2 softmax); a per-tensor K scale is a
     // device float, so the kernel folds it into q after reading it.
-    const float qs = static_cast<float>(scale) * kLog2e;
+    p.q_scale = static_cast<float>(scale) * kLog2e;
+
     auto s = reinterpret_cast<hipStream_t>(stream);
-    const int wpg = (n_kv_heads % 4 == 0) ? 4 : (n_kv_heads % 2 == 0) ? 2 : 1;   // waves (kv heads) per group
-    const dim3 grid(static_cast<unsigned>(num_tokens), static_cast<unsigned>(n_kv_heads / wpg),
-                    static_cast<unsigned>(ms));
-    const int st = split_tokens / kTileKeys;
-    bool ok = true;
-    if (phase & kPhaseSplit) {
-    if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD) {
-        ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
-                                                                        k_scale, v_scale, block_tables, table_width,
-                                                                        token_seq, token_kv_len, n_kv_heads, lg, st,
-                                                                        static_cast<int>(ms), qs)
-                             : launch_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
-                                                                       k_scale, v_scale, block_tables, table_width,
-                                                                       token_seq, token_kv_len, n_kv_heads, lg, st,
-                                                                       static_cast<int>(ms), qs);
-    } else {
-        ok = head_dim == 128 ? launch_rep<128, CVH_SCALE_PER_TENSOR>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
-                                                                    k_scale, v_scale, block_tables, table_width,
-                                                                    token_seq, token_kv_len, n_kv_heads, lg, st,
-                                                                    static_cast<int>(ms), qs)
-                             : launch_rep<64, CVH_SCALE_PER_TENSOR>(rep, grid, 64 * wpg, s, out, pa, pm, q, k_cache, v_cache,
-                                                                   k_scale, v_scale, block_tables, table_width,
-                                                                   token_seq, token_kv_len, n_kv_heads, lg, st,
-                                                                   static_cast<int>(ms), qs);
+    if (phase & kPhaseDecode) {
+        const size_t lds = static_cast<size_t>(rows + 1) * sizeof(int);
+        const bool one_block = (1 << lg) >= kTileKeys;
+        bool ok;
+        if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
+            ok = head_dim == 128
+                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block)
+                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block);
+        else
+            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block)
+                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block);
+        if (!ok) return CVH_ERR_UNSUPPORTED;
+        if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
-    }
-    if (!ok) return CVH_ERR_UNSUPPORTED;
-    if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
-    if (ms > 1 && (phase & kPhaseMerge)) {
+    if ((phase & kPhaseMerge) && G > 1) {
         const dim3 mgrid(static_cast<unsigned>(n_heads), static_cast<unsigned>(num_tokens));
-        auto* o = static_cast<uint16_t*>(out);
+        const int nt = static_cast<int>(num_tokens);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 64, 0, s>>>(o, pa, pm, token_kv_len, v_scale, table_width, lg, n_heads, st, static_cast<int>(ms));
+                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 64, 0, s>>>(
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
             else
-                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, 64, 0, s>>>(o, pa, pm, token_kv_len, v_scale, table_width, lg, n_heads, st, static_cast<int>(ms));
+                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, 64, 0, s>>>(
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
         } else {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 64, 0, s>>>(o, pa, pm, token_kv_len, v_scale, table_width, lg, n_heads, st, static_cast<int>(ms));
+                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 64, 0, s>>>(
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
             else
-                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, 64, 0, s>>>(o, pa, pm, token_kv_len, v_scale, table_width, lg, n_heads, st, static_cast<int>(ms));
+                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, 64, 0, s>>>(
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
         }
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
     return CVH_OK;
 }
+
 }  // namespace
 }  // namespace cvh
 
-#define CVH_PA_ARGS                                                                                                   \
-    out, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq, token_kv_len, num_tokens,      \
-            n_heads, n_kv_heads, head_dim, block_size, scale_mode, scale, split_tokens, workspace, workspace_bytes,  \
+extern "C" int cvh_paged_attention_partitions(int64_t num_tokens, int n_kv_heads, int64_t table_width,
+                                              int block_size) {
+    if (num_tokens <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0) return 1;
+    return cvh::auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
+}
+
+extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                                      int64_t table_width, int block_size, int partitions) {
+    if (num_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0 ||
+        partitions < 0 || n_heads % n_kv_heads != 0)
+        return 0;
+    const int G = partitions ? partitions : cvh::auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
+    return cvh::ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G).total;
+}
+
+#define CVH_PA_ARGS                                                                                                  \
+    out, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq, token_kv_len, num_tokens,     \
+            n_heads, n_kv_heads, head_dim, block_size, scale_mode, scale, partitions, workspace, workspace_bytes,    \
             stream
-#define CVH_PA_PARAMS                                                                                                 \
-    void *out, const void *q, const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,                 \
-            const float *v_scale, const int64_t *block_tables, int64_t table_width, const int64_t *token_seq,        \
-            const int64_t *token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,              \
-            int block_size, int scale_mode, double scale, int split_tokens, void *workspace, size_t workspace_bytes, \
+#define CVH_PA_PARAMS                                                                                                \
+    void *out, const void *q, const uint8_t *k_cache, const uint8_t *v_cache, const float *k_scale,                \
+            const float *v_scale, const int64_t *block_tables, int64_t table_width, const int64_t *token_seq,       \
+            const int64_t *token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,             \
+            int block_size, int scale_mode, double scale, int partitions, void *workspace, size_t workspace_bytes,  \
             cvh_stream_t stream
 
 extern "C" int cvh_paged_attention_fp8_ex(CVH_PA_PARAMS) {
     return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseBoth);
 }
 extern "C" int cvh_paged_attention_fp8_split_phase(CVH_PA_PARAMS) {
-    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseSplit);
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseDecode);
 }
 extern "C" int cvh_paged_attention_fp8_merge_phase(CVH_PA_PARAMS) {
     return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseMerge);

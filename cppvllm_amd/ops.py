@@ -43,15 +43,15 @@ def _scale_mode(k_scale: torch.Tensor) -> int:
 
 
 def paged_attention_workspace(num_tokens: int, n_heads: int, n_kv_heads: int, head_dim: int, table_width: int,
-                              block_size: int, split_tokens: int = 0, device="cuda") -> torch.Tensor:
+                              block_size: int, partitions: int = 0, device="cuda") -> torch.Tensor:
     """Preallocated split-K workspace (what the reference allocates per call, paged_attention.cu:415-421)."""
     n = _lib.lib().cvh_paged_attention_workspace_bytes(num_tokens, n_heads, n_kv_heads, head_dim, table_width,
-                                                      block_size, split_tokens)
+                                                      block_size, partitions)
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
 def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len,
-                        scale: float, *, workspace: torch.Tensor | None = None, split_tokens: int = 0) -> None:
+                        scale: float, *, workspace: torch.Tensor | None = None, partitions: int = 0) -> None:
     """FP8 paged attention over a ragged batch of query tokens (kernels/paged_attention.cu:459-473).
 
     out, q: bf16 [T, H, HD]; k_cache, v_cache: uint8 [NB, BS, KV, HD]; k_scale, v_scale: float32
@@ -66,11 +66,11 @@ def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables
     BS, KV = k_cache.size(1), k_cache.size(2)
     W = block_tables.size(1)
     if workspace is None:
-        workspace = paged_attention_workspace(T, H, KV, HD, W, BS, split_tokens, q.device)
+        workspace = paged_attention_workspace(T, H, KV, HD, W, BS, partitions, q.device)
     code = _lib.lib().cvh_paged_attention_fp8_ex(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
         v_scale.data_ptr(), block_tables.data_ptr(), W, token_seq.data_ptr(), token_kv_len.data_ptr(), T, H, KV,
-        HD, BS, _scale_mode(k_scale), float(scale), int(split_tokens), workspace.data_ptr(),
+        HD, BS, _scale_mode(k_scale), float(scale), int(partitions), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream(q))
     check("paged_attention_fp8", code)
 

@@ -59,9 +59,10 @@ enum { CVH_DTYPE_BF16 = 0, CVH_DTYPE_F16 = 1, CVH_DTYPE_F32 = 2 };
  *                                    a token with kv_len <= 0 gets an all-zero output row
  *   scale        softmax scale (1/sqrt(head_dim) in the reference)
  * Supported: head_dim in {64,128}; n_heads/n_kv_heads in {1,2,4,8}; block_size a power of two
- * in [16, 4096]. Queries of one sequence may be several tokens (chunked-prefill continuation).
+ * in [16, 4096]; num_tokens * n_kv_heads / 4 <= 16383 (rounded up for 1 or 2 kv heads).
+ * Queries of one sequence may be several tokens (chunked-prefill continuation).
  * workspace: device memory of at least cvh_paged_attention_workspace_bytes(...) bytes for the
- * same arguments (split-K partials). Its contents need no initialisation.
+ * same arguments (tile prefix and split partials). Its contents need no initialisation.
  * ------------------------------------------------------------------------------------------- */
 int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
                             const float* k_scale, const float* v_scale, const int64_t* block_tables,
@@ -70,44 +71,46 @@ int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, co
                             int scale_mode, double scale, void* workspace, size_t workspace_bytes,
                             cvh_stream_t stream);
 
-/* Same as cvh_paged_attention_fp8 with an explicit split-K chunk: every query token's context is
- * cut into splits of split_tokens keys (a multiple of 32, >= 64); 0 = automatic choice.
- * (No reference counterpart for the knob: the reference hard-codes its split heuristic,
- *  kernels/paged_attention.cu:403-409; tests use it to prove split invariance.) */
+/* Same as cvh_paged_attention_fp8 with an explicit work partition count: the concatenated
+ * 32-key tiles of all (token, kv-head group) rows are cut into `partitions` equal ranges, one
+ * workgroup each; 0 = automatic (one per resident workgroup slot of an MI355X, fewer for small
+ * batches). Results agree to fp32 rounding for every partition count.
+ * (No reference counterpart for the knob: the reference hard-codes a split heuristic,
+ *  kernels/paged_attention.cu:403-409; tests use it to prove partition invariance.) */
 int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
                                const float* k_scale, const float* v_scale, const int64_t* block_tables,
                                int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
                                int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
-                               int scale_mode, double scale, int split_tokens, void* workspace,
+                               int scale_mode, double scale, int partitions, void* workspace,
                                size_t workspace_bytes, cvh_stream_t stream);
 
 /* The two launches of cvh_paged_attention_fp8_ex, exposed separately (same arguments; run on one
- * stream, split phase first): the split phase runs the decode kernel, which writes the output of
- * every token whose context fits one split and (acc, max, sum) partials for the others; the
- * merge phase combines those partials (no-op when no token can have two splits). Callers use
- * them to time the decode kernel alone or to interleave other work between the phases.
+ * stream, split phase first): the split phase runs the decode kernel, which finishes every
+ * (token, head) whose keys one workgroup covered and writes (acc, max, sum) partials for the
+ * others; the merge phase combines those partials. Callers use them to time the decode kernel
+ * alone or to interleave other work between the phases.
  * (No reference counterpart: the reference launches both back to back,
  *  kernels/paged_attention.cu:423-441.) */
 int cvh_paged_attention_fp8_split_phase(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
                                         const float* k_scale, const float* v_scale, const int64_t* block_tables,
                                         int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
                                         int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                                        int block_size, int scale_mode, double scale, int split_tokens,
+                                        int block_size, int scale_mode, double scale, int partitions,
                                         void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 int cvh_paged_attention_fp8_merge_phase(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
                                         const float* k_scale, const float* v_scale, const int64_t* block_tables,
                                         int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
                                         int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                                        int block_size, int scale_mode, double scale, int split_tokens,
+                                        int block_size, int scale_mode, double scale, int partitions,
                                         void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 
 /* Workspace bytes needed by the calls above (replaces the per-call at::empty of
  * kernels/paged_attention.cu:415-421, which cannot run under graph capture). */
 size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                                           int64_t table_width, int block_size, int split_tokens);
+                                           int64_t table_width, int block_size, int partitions);
 
-/* The split chunk (keys per split) the automatic policy picks for these shapes. */
-int cvh_paged_attention_split_tokens(int64_t num_tokens, int n_kv_heads, int64_t table_width, int block_size);
+/* The partition count the automatic policy picks for these shapes. */
+int cvh_paged_attention_partitions(int64_t num_tokens, int n_kv_heads, int64_t table_width, int block_size);
 
 /* ---------------------------------------------------------------------------------------------
  * RMSNorm family. Replaces fused::rms_norm / fused::add_rms_norm (kernels/fused_ops.h:7-9,

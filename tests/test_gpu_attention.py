@@ -18,11 +18,11 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def run_gpu(b, split_tokens=0):
+def run_gpu(b, partitions=0):
     out = torch.empty_like(b["q"])
     ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
                             b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
-                            split_tokens=split_tokens)
+                            partitions=partitions)
     torch.cuda.synchronize()
     return bits(out)
 
@@ -93,9 +93,9 @@ def test_shapes_and_boundaries(orc, BS, H, KV, HD, per_tensor):
     assert_close_bf16(got, want)
 
 
-@pytest.mark.parametrize("split", [64, 96, 256, 2048])
-def test_split_invariance(orc, split):
-    say(f"split invariance split_tokens={split}")
+@pytest.mark.parametrize("split", [1, 2, 7, 64, 511, 4096])
+def test_partition_invariance(orc, split):
+    say(f"partition invariance partitions={split}")
     b = synth(11, [70, 600, 1500, 2100, 3000], 16)
     db = dev(b)
     base = run_gpu(db, 0)
@@ -169,7 +169,7 @@ def test_workspace_contract():
     with pytest.raises(_lib.CvhError) as e:
         ops.paged_attention_fp8(torch.empty_like(b["q"]), b["q"], b["k_cache"], b["v_cache"], b["k_scale"],
                                 b["v_scale"], b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
-                                workspace=small, split_tokens=64)
+                                workspace=small, partitions=64)
     assert e.value.code == _lib.CVH_ERR_WORKSPACE
 
 
@@ -185,7 +185,7 @@ def test_workspace_reused():
         out = torch.empty_like(b["q"])
         ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
                                 b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"], workspace=ws,
-                                split_tokens=64)
+                                partitions=64)
         torch.cuda.synchronize()
         outs.append(bits(out))
     assert np.array_equal(outs[0], outs[1])

@@ -39,27 +39,31 @@ def test_argument_validation_without_device():
     assert lib.cvh_paged_attention_fp8(*args, 4, p, p, 4, 24, 8, 128, 16, 0, 0.1, None, 0, None) == unsup
     assert lib.cvh_paged_attention_fp8(*args, 4, p, p, 4, 16, 8, 128, 24, 0, 0.1, None, 0, None) == unsup
     assert lib.cvh_paged_attention_fp8(*args, 4, p, p, 4, 16, 8, 128, 8, 0, 0.1, None, 0, None) == unsup
-    assert lib.cvh_paged_attention_fp8_ex(*args, 4, p, p, 4, 16, 8, 128, 16, 0, 0.1, 48, None, 0, None) == bad
-    # workspace missing for a split launch
+    assert lib.cvh_paged_attention_fp8_ex(*args, 4, p, p, 4, 16, 8, 128, 16, 0, 0.1, -3, None, 0, None) == bad
+    # workspace missing
     assert lib.cvh_paged_attention_fp8_ex(*args, 8, p, p, 4, 16, 8, 128, 16, 0, 0.1, 64, None, 0,
                                           None) == _lib.CVH_ERR_WORKSPACE
+    # too many rows for one launch
+    assert lib.cvh_paged_attention_fp8(*args, 1, p, p, 20000, 16, 8, 128, 16, 0, 0.1, p, 1 << 30,
+                                       None) == unsup
     assert lib.cvh_rms_norm(p, p, p, 3, 1020, 1e-6, 0, None) == unsup
     assert lib.cvh_rms_norm(p, p, p, 3, 1024, 1e-6, 7, None) == unsup
     assert lib.cvh_qk_norm_rope_kv_write_fp8(*[p] * 14, 4, 16, 8, 96, 16, 0, 1e-6, None) == unsup
     assert lib.cvh_qk_norm_rope_kv_write_fp8(*[p] * 14, 4, 16, 8, 128, 20, 0, 1e-6, None) == unsup
 
 
-def test_split_policy_and_workspace_sizes():
+def test_partition_policy_and_workspace_sizes():
     lib = _lib.lib()
-    # headline decode (256 tokens, 8 kv heads, 8 x 256-token blocks): 512-key chunks, 4 splits max
-    assert lib.cvh_paged_attention_split_tokens(256, 8, 8, 256) == 512
-    assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == 256 * 16 * 4 * 130 * 4
-    # a small batch shrinks the chunk to fill the GPU, never below 64 keys
-    assert lib.cvh_paged_attention_split_tokens(8, 8, 4, 256) == 64
-    assert lib.cvh_paged_attention_split_tokens(1, 1, 1, 16) == 64
-    # one split => no workspace
-    assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 1, 16, 64) == 0
-    assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 8, 16, 48) == 0   # invalid split
+    # headline decode (256 tokens, 8 kv heads = 2 row groups, 8 x 256-token blocks): 512 partitions
+    assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 512
+    rows, slots = 256 * 2, 512 * 2 * 8     # [G][2][WPG*REP] partial slots
+    r256 = lambda v: (v + 255) // 256 * 256
+    want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4)
+    assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == want
+    # small batches: never less than two tiles per partition
+    assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
+    assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 8 * 2 * 32 // 2
+    assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 8, 16, -1) == 0
 
 
 def test_rope_tables_reject_bad_args():
