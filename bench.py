@@ -82,6 +82,7 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--partitions", type=int, default=0, help="work partitions (0 = automatic)")
+    ap.add_argument("--eager", action="store_true", help="launch eagerly instead of replaying HIP graphs")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain 1 GiB device-to-device copies (rocprofv3 FETCH/WRITE_SIZE scale)")
     args = ap.parse_args()
@@ -118,51 +119,63 @@ def main():
             layers.append(tuple(x.clone() for x in (b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"])))
     lib = _lib.lib()
     ws_bytes = lib.cvh_paged_attention_workspace_bytes(T, H, KV, HD, W, BS, args.partitions)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
     out = torch.empty_like(b["q"])
-    stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
-    fixed = (out.data_ptr(), b["q"].data_ptr())
-    tail = (b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(), b["token_kv_len"].data_ptr(), T, H, KV, HD,
-            BS, _lib.SCALE_PER_TOKEN_HEAD, b["scale"], args.partitions, ws.data_ptr(), ws_bytes, sp)
     layer_ptrs = [tuple(x.data_ptr() for x in lay) for lay in layers]
-    # the op = decode kernel (split phase) + split merge (merge phase), launched back to back
+    # the op = decode kernel (split phase) + merge of cut rows (merge phase)
     split_fn = lib.cvh_paged_attention_fp8_split_phase
     merge_fn = lib.cvh_paged_attention_fp8_merge_phase
 
-    def layer(lp, ev=None):
-        code = split_fn(*fixed, *lp, *tail)
-        if ev is not None:
-            ev.record(stream)
-        code = code or merge_fn(*fixed, *lp, *tail)
+    def launch(fn, lp):
+        sp = torch.cuda.current_stream(dev).cuda_stream      # the capture stream during capture
+        code = fn(out.data_ptr(), b["q"].data_ptr(), *lp, b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(),
+                  b["token_kv_len"].data_ptr(), T, H, KV, HD, BS, _lib.SCALE_PER_TOKEN_HEAD, b["scale"],
+                  args.partitions, ws.data_ptr(), ws_bytes, sp)
         if code:
             raise _lib.CvhError("paged_attention_fp8", code)
 
-    def step():
+    def step():                   # one decode step: 28 layers, each decode + merge
         for lp in layer_ptrs:
-            layer(lp)
+            launch(split_fn, lp)
+            launch(merge_fn, lp)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # events around every decode-kernel launch of the timed region, on the stream it runs on
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps * len(layer_ptrs))]
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record(stream)
-    i = 0
-    for _ in range(args.steps):
+    def decode_only():            # the dominant kernel alone, 28 launches back to back
         for lp in layer_ptrs:
-            evs[i][0].record(stream)
-            layer(lp, evs[i][1])
-            i += 1
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    layer_ms = [a.elapsed_time(z) for a, z in evs]
-    avg_layer_ms = sum(layer_ms) / len(layer_ms)
+            launch(split_fn, lp)
+
+    def capture(fn):
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    def timed(replay, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    if args.eager:
+        run_step, run_decode = step, decode_only
+    else:                         # HIP graphs, as a decode engine replays them
+        g_step, g_dec = capture(step), capture(decode_only)
+        run_step, run_decode = g_step.replay, g_dec.replay
+    for _ in range(args.warmup):
+        run_step()
+    total_ms = timed(run_step, args.steps)
+    # events bracket K back-to-back replays of the 28 decode-kernel launches (same stream)
+    dec_ms = timed(run_decode, args.steps)
+    avg_layer_ms = dec_ms / (args.steps * len(layer_ptrs))
 
     bytes_layer = workloads.attention_bytes(lens)
     bytes_step = bytes_layer * len(layer_ptrs)
@@ -189,10 +202,12 @@ def main():
             "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, KV, W, BS)
             if args.partitions == 0 else args.partitions,
             "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "launch": "eager" if args.eager else "hip_graph",
+            "op_us_per_layer": round(total_ms * 1e3 / (args.steps * len(layer_ptrs)), 2),
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "paged_decode_kernel (split phase of the op; the merge kernel is excluded)",
+                     "kernel": "paged_decode_kernel (split phase; graph of 28 back-to-back launches)",
                      "avg_launch_us": round(avg_layer_ms * 1e3, 2)},
     }
     if not args.no_cpu:

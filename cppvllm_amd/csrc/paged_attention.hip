@@ -467,20 +467,21 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(Params p) {
     }
 }
 
-// Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One wave per
-// (token, query head); it recomputes which workgroups covered the row from the prefix the decode
-// kernel stored, and exits for rows finished in place.
+// Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One workgroup
+// per row (token, kv-head group): it recomputes, from the prefix the decode kernel stored, which
+// workgroups covered the row (wave-uniform scalar arithmetic) and exits if one did. Otherwise
+// thread i handles query head i / (HD/4) of the row and 4 consecutive dims; the pieces are
+// combined in one online pass (running max), so their loads are independent of each other.
 template <int HD, int SM>
-__global__ __launch_bounds__(64) void paged_merge_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
-                                                         const float* __restrict__ part_ml,
-                                                         const int* __restrict__ prefix,
-                                                         const float* __restrict__ v_scale, int num_tokens, int n_kv,
-                                                         int rep, int wpg, int G) {
-    const int h = blockIdx.x;
-    const int t = blockIdx.y;
-    const int g = h / rep, rr = h % rep;
+__global__ __launch_bounds__(256) void paged_merge_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
+                                                          const float* __restrict__ part_ml,
+                                                          const int* __restrict__ prefix,
+                                                          const float* __restrict__ v_scale, int num_tokens, int n_kv,
+                                                          int rep, int wpg, int G) {
+    constexpr int TPH = HD / 4;                       // threads per query head
+    const int row = blockIdx.x;
     const int hg_count = n_kv / wpg;
-    const int row = t * hg_count + g / wpg, wi = g % wpg;
+    const int heads_per_row = wpg * rep;             // query heads of one row group
     const int rows = num_tokens * hg_count;
     const int64_t U = prefix[rows];
     const int64_t pr0 = prefix[row], pr1 = prefix[row + 1];
@@ -489,33 +490,36 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(uint16_t* __restrict__ 
     auto owner = [&](int64_t u) { return static_cast<int>(((u + 1) * G - 1) / U); };
     const int w0 = owner(pr0), w1 = owner(pr1 - 1);
     if (w0 == w1) return;
-    // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
-    float M = kMinusHuge;
-    for (int w = w0; w <= w1; ++w) {
-        if (w * U / G == (w + 1) * U / G) continue;
-        const int slot = (pr0 <= w * U / G) ? 0 : 1;
-        const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * rep + rr;
-        M = fmaxf(M, reinterpret_cast<const float2*>(part_ml)[idx].x);
+    const int t = row / hg_count, hgi = row % hg_count;
+    const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
+    for (int hh = threadIdx.x / TPH; hh < heads_per_row; hh += blockDim.x / TPH) {
+        const int d0 = (threadIdx.x % TPH) * 4;
+        float M = kMinusHuge, L = 0.f;
+        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+        for (int w = w0; w <= w1; ++w) {
+            // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
+            if (w * U / G == (w + 1) * U / G) continue;
+            const int slot = (pr0 <= w * U / G) ? 0 : 1;
+            const int64_t idx = (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh;
+            const float2 ml = reinterpret_cast<const float2*>(part_ml)[idx];
+            const float4 a = *reinterpret_cast<const float4*>(part_acc + idx * HD + d0);
+            const float Mn = fmaxf(M, ml.x);
+            const float co = exp2f(M - Mn), cn = exp2f(ml.x - Mn);
+            L = L * co + ml.y * cn;
+            A.x = A.x * co + a.x * cn;
+            A.y = A.y * co + a.y * cn;
+            A.z = A.z * co + a.z * cn;
+            A.w = A.w * co + a.w * cn;
+            M = Mn;
+        }
+        const float f = vfin / L;
+        const int h = hgi * heads_per_row + hh;      // query head index within the token
+        uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
+        const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
+        const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
+        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
     }
-    constexpr int PER = HD / 64;
-    float L = 0.f, A[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) A[i] = 0.f;
-    for (int w = w0; w <= w1; ++w) {
-        if (w * U / G == (w + 1) * U / G) continue;
-        const int slot = (pr0 <= w * U / G) ? 0 : 1;
-        const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * rep + rr;
-        const float2 ml = reinterpret_cast<const float2*>(part_ml)[idx];
-        const float c = exp2f(ml.x - M);
-        L += ml.y * c;
-        const float* pa = part_acc + idx * HD;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) A[i] += pa[threadIdx.x + 64 * i] * c;
-    }
-    const float f = ((SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f) / L;
-    uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) o[threadIdx.x + 64 * i] = f32_to_bf16_bits(A[i] * f);
 }
 
 // ---- host side ------------------------------------------------------------------------------------
@@ -645,21 +649,21 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
     if ((phase & kPhaseMerge) && G > 1) {
-        const dim3 mgrid(static_cast<unsigned>(n_heads), static_cast<unsigned>(num_tokens));
+        const dim3 mgrid(static_cast<unsigned>(rows));
         const int nt = static_cast<int>(num_tokens);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 64, 0, s>>>(
+                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 256, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
             else
-                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, 64, 0, s>>>(
+                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, 256, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
         } else {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 64, 0, s>>>(
+                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 256, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
             else
-                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, 64, 0, s>>>(
+                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, 256, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
         }
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
