@@ -83,6 +83,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--partitions", type=int, default=0, help="work partitions (0 = automatic)")
     ap.add_argument("--eager", action="store_true", help="launch eagerly instead of replaying HIP graphs")
+    ap.add_argument("--config", type=int, default=3, choices=(3, 4),
+                    help="3: 256 seqs, ctx U(100,1024)+U(0,1024) (headline); 4: 64 seqs, ctx log-U(4k,32k)")
+    ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain 1 GiB device-to-device copies (rocprofv3 FETCH/WRITE_SIZE scale)")
     args = ap.parse_args()
@@ -106,8 +109,11 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibration": "3 x 1 GiB device copy", "bytes_per_copy": 1 << 30}))
         return
-    print("bench: building config 3 on device", flush=True, file=sys.stderr)
-    b = workloads.config3(device=dev)
+    print(f"bench: building config {args.config} on device", flush=True, file=sys.stderr)
+    if args.config == 3:
+        b = workloads.config3(device=dev)
+    else:
+        b = workloads.config4(device=dev, shared_prefix=args.shared_prefix)
     lens = b["token_kv_len"].cpu().tolist()
     T, H, KV, HD, BS = len(lens), b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
     W = b["block_tables"].shape[1]
@@ -196,7 +202,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded N(0,1) K/V quantised to e4m3 per (token, head); random block tables)",
         "config": {
-            "workload": "BASELINE config 3: 256-seq FP8 paged decode step, 28 layers, distinct per-layer caches",
+            "workload": ("BASELINE config 3: 256-seq FP8 paged decode step, 28 layers, distinct per-layer caches"
+                         if args.config == 3 else
+                         "BASELINE config 4%s: 64-seq long-context FP8 paged decode, 28 layers, distinct per-layer "
+                         "caches" % ("b (shared 8-block prefix)" if args.shared_prefix else "")),
             "seqs": T, "ctx_sum": int(sum(lens)), "ctx_min": int(min(lens)), "ctx_max": int(max(lens)),
             "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "block_size": BS, "layers": len(layer_ptrs),
             "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, KV, W, BS)

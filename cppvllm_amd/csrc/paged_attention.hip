@@ -76,10 +76,18 @@ __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNonTemporal));
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 template <int HD> struct KvVec;
 template <> struct KvVec<128> {
     using T = uint4;
     static constexpr int kElems = 16;
+    static __device__ __forceinline__ void words(const uint4& u, uint32_t (&w)[4]) {
+        w[0] = u.x;
+        w[1] = u.y;
+        w[2] = u.z;
+        w[3] = u.w;
+    }
     static __device__ __forceinline__ void to_f32(const uint4& u, float (&f)[16]) {
         fp8x4_to_f32(u.x, f + 0);
         fp8x4_to_f32(u.y, f + 4);
@@ -90,6 +98,10 @@ template <> struct KvVec<128> {
 template <> struct KvVec<64> {
     using T = uint2;
     static constexpr int kElems = 8;
+    static __device__ __forceinline__ void words(const uint2& u, uint32_t (&w)[2]) {
+        w[0] = u.x;
+        w[1] = u.y;
+    }
     static __device__ __forceinline__ void to_f32(const uint2& u, float (&f)[8]) {
         fp8x4_to_f32(u.x, f + 0);
         fp8x4_to_f32(u.y, f + 4);
@@ -136,6 +148,15 @@ __device__ __forceinline__ float across_groups_max(float v) {
     return xor32_max(v);
 }
 
+// Wave-uniform read of kernel-constant data (block tables, token metadata) through the constant
+// address space, which makes it a scalar load (s_load) even though the pointer cannot be proven
+// free of aliasing with the kernel's stores; vector loads here would share the vmcnt counter with
+// the K/V stream and force full waits.
+template <typename T> __device__ __forceinline__ T ld_uniform(const T* ptr, int64_t i) {
+    typedef const T __attribute__((address_space(4)))* cptr;
+    return ((cptr)(uintptr_t)ptr)[i];
+}
+
 struct Params {
     uint16_t* out;
     float* part_acc;         // [G][2][WPG][REP][HD]
@@ -164,181 +185,12 @@ __device__ __forceinline__ int token_len(const Params& p, int t) {
     if (kv > cap) kv = cap;
     return kv > 0 ? static_cast<int>(kv) : 0;
 }
-
-// Attention of one wave (kv head g, REP query heads of token t) over tiles [tb, te) of the
-// token's context. Returns the piece's wave max m, sum l and unnormalised acc (valid in all
-// lanes; lane `sub` holds dims sub*E .. sub*E+E-1).
-template <int HD, int REP, int SM, bool ONE_BLOCK>
-__device__ __forceinline__ void scan_tiles(const Params& p, int t, int g, int kv_len, int tb, int te, float (&m)[REP],
-                                           float (&l)[REP], float (&acc)[REP][KvVec<HD>::kElems]) {
-    using V = KvVec<HD>;
-    using VT = typename V::T;
-    constexpr int E = V::kElems;
-    const int lane = threadIdx.x & 63;
-    const int grp = lane >> 3;
-    const int sub = lane & 7;
-    const int H = p.n_kv * REP;
-    const int log2_bs = p.log2_bs;
-    const int64_t* table = p.block_tables + p.token_seq[t] * p.table_width;
-    const uint32_t row_bytes = static_cast<uint32_t>(p.n_kv) * HD;   // bytes of one slot (all kv heads)
-    const int64_t blk_bytes = static_cast<int64_t>(row_bytes) << log2_bs;
-    const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
-    const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
-    const int bs_mask = (1 << log2_bs) - 1;
-    const uint32_t lane_col = g * HD + sub * E;                     // byte column inside a slot row
-
-    // q slice for the REP heads of this kv head, pre-scaled by scale*log2(e) [*k_scale]
-    const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? p.q_scale * p.k_scale[0] : p.q_scale;
-    float qf[REP][E];
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        const uint16_t* qr = p.q + ((int64_t)t * H + g * REP + r) * HD + sub * E;
-#pragma unroll
-        for (int c = 0; c < E / 8; ++c) {
-            const uint4 u = reinterpret_cast<const uint4*>(qr)[c];
-            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qf[r][c * 8 + 2 * i] = bf16_bits_to_f32(w[i] & 0xffffu) * qsc;
-                qf[r][c * 8 + 2 * i + 1] = bf16_bits_to_f32(w[i] >> 16) * qsc;
-            }
-        }
-    }
-    // running max per key group; a finite floor so an all-masked group gives exp2(-inf) = 0
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        m[r] = kMinusHuge;
-        l[r] = 0.f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[r][e] = 0.f;
-    }
-
-    struct Tile {
-        VT k[kSteps], v[kSteps];
-        float ks[kSteps], vs[kSteps];
-    };
-    // Physical blocks of a tile: `lo` for its first 16 keys, `hi` for the last 16 (equal unless
-    // block_size == 16). Wave-uniform scalar loads, looked up one tile ahead of use.
-    struct Phys {
-        int64_t lo, hi;
-    };
-    auto lookup = [&](int tile) -> Phys {
-        tile = min(tile, te - 1);
-        const int p0 = tile * kTileKeys;
-        const int64_t lo = max(table[p0 >> log2_bs], int64_t{0});
-        if constexpr (ONE_BLOCK) return {lo, lo};
-        const int64_t hi = max(table[min(p0 + kTileKeys / 2, kv_len - 1) >> log2_bs], int64_t{0});
-        return {lo, hi};
-    };
-    // Keys past kv_len (last tile only) are clamped to key kv_len-1: a valid, finite row whose
-    // score is masked. live = false: the prefetch past the piece's end (zero-size descriptors).
-    auto load_tile = [&](int tile, Tile& tl, Phys ph2, bool live) {
-        const int p0 = tile * kTileKeys;
-        const uint32_t lv = static_cast<uint32_t>(live);            // arithmetic, not a branch
-        const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            const int64_t ph = (ONE_BLOCK || s < kSteps / 2) ? ph2.lo : ph2.hi;
-            const int pos = min(p0 + 8 * s + grp, kv_len - 1);
-            const uint32_t in_blk = static_cast<uint32_t>(pos & bs_mask);
-            const uint32_t off = in_blk * row_bytes + lane_col;
-            tl.k[s] = buf_load<VT>(make_rsrc(p.k_cache + ph * blk_bytes, kv_rec), off);
-            tl.v[s] = buf_load<VT>(make_rsrc(p.v_cache + ph * blk_bytes, kv_rec), off);
-            if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
-                const int64_t sbase = (ph * p.n_kv + g) << log2_bs;
-                tl.ks[s] = buf_load_f32(make_rsrc(p.k_scale + sbase, s_rec), in_blk * 4u);
-                tl.vs[s] = buf_load_f32(make_rsrc(p.v_scale + sbase, s_rec), in_blk * 4u);
-            } else {
-                tl.ks[s] = 1.f;
-                tl.vs[s] = 1.f;
-            }
-        }
-    };
-    auto compute = [&](int tile, const Tile& tl) {
-        const int p0 = tile * kTileKeys;
-        float sc[REP][kSteps];
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            float kf[E];
-            V::to_f32(tl.k[s], kf);
-#pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < E; ++e) d += qf[r][e] * kf[e];
-                sc[r][s] = d;
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            const bool valid = (p0 + 8 * s + grp) < kv_len;
-#pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                float d = group8_sum(sc[r][s]);
-                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) d *= tl.ks[s];
-                sc[r][s] = valid ? d : -INFINITY;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            float mt = sc[r][0];
-#pragma unroll
-            for (int s = 1; s < kSteps; ++s) mt = fmaxf(mt, sc[r][s]);
-            const bool need = mt > m[r] + kRescaleThreshold;    // per key group
-            if (__builtin_amdgcn_ballot_w64(need) != 0) {      // wave-uniform; rare after tile 0
-                const float mn = need ? mt : m[r];
-                const float c = __builtin_amdgcn_exp2f(m[r] - mn);
-                l[r] *= c;
-#pragma unroll
-                for (int e = 0; e < E; ++e) acc[r][e] *= c;
-                m[r] = mn;
-            }
-#pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
-                const float pr = __builtin_amdgcn_exp2f(sc[r][s] - m[r]);
-                l[r] += pr;
-                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) sc[r][s] = pr * tl.vs[s];
-                else sc[r][s] = pr;
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            float vf[E];
-            V::to_f32(tl.v[s], vf);
-#pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                const float w = sc[r][s];
-#pragma unroll
-                for (int e = 0; e < E; ++e) acc[r][e] += w * vf[e];
-            }
-        }
-    };
-
-    Tile ta, tbuf;
-    Phys pa = lookup(tb);
-    Phys pb = lookup(tb + 1);
-    load_tile(tb, ta, pa, true);
-    for (int tile = tb;; tile += 2) {
-        load_tile(min(tile + 1, te - 1), tbuf, pb, tile + 1 < te);
-        pa = lookup(tile + 2);
-        compute(tile, ta);
-        if (tile + 1 >= te) break;
-        load_tile(min(tile + 2, te - 1), ta, pa, tile + 2 < te);
-        pb = lookup(tile + 3);
-        compute(tile + 1, tbuf);
-        if (tile + 2 >= te) break;
-    }
-
-    // combine the 8 key groups: rescale each to the wave max, then sum
-#pragma unroll
-    for (int r = 0; r < REP; ++r) {
-        const float M = across_groups_max(m[r]);
-        const float c = __builtin_amdgcn_exp2f(m[r] - M);
-        m[r] = M;
-        l[r] = across_groups_sum(l[r] * c);   // l is uniform inside a group
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[r][e] = across_groups_sum(acc[r][e] * c);
-    }
+// The same for a wave-uniform t (scalar load).
+__device__ __forceinline__ int token_len_uniform(const Params& p, int t) {
+    int64_t kv = ld_uniform(p.token_kv_len, t);
+    const int64_t cap = p.table_width << p.log2_bs;
+    if (kv > cap) kv = cap;
+    return kv > 0 ? static_cast<int>(kv) : 0;
 }
 
 // Exclusive prefix of row tile counts into LDS (prefix[0..rows]); all threads of the block.
@@ -375,9 +227,18 @@ __device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int 
     __syncthreads();
 }
 
+// One piece of work of a workgroup: tiles [lt, le) of row `row` (token t, kv head g of this wave).
+// row < 0 marks "no more work" (its other fields are safe dummies: loads made for it use zero-size
+// descriptors, and its table lookups stay inside block-table row 0).
+struct Piece {
+    int row, t, g, kv_len, lt, le;
+    int64_t seq;   // block-table row of token t
+};
+
 template <int HD, int REP, int SM, bool ONE_BLOCK>
-__global__ __launch_bounds__(256) void paged_decode_kernel(Params p) {
+__global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
     using V = KvVec<HD>;
+    using VT = typename V::T;
     constexpr int E = V::kElems;
     extern __shared__ int prefix[];
     const int wpg = p.wpg;
@@ -387,82 +248,335 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(Params p) {
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
 
-    const int64_t U = prefix[rows];
+    // prefix values are the same for every lane; uniform() makes that visible to the compiler so
+    // all the piece bookkeeping below stays in scalar registers
+    auto uniform = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    auto pfx = [&](int i) { return uniform(prefix[i]); };
+    const int64_t U = pfx(rows);
     const int64_t G = gridDim.x;
     const int w = blockIdx.x;
     const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
     const bool last_wg = (w == G - 1);
     const int lane = threadIdx.x & 63;
-    const int sub = lane & 7;
     const int grp = lane >> 3;
+    const int sub = lane & 7;
     // wave-uniform by construction; readfirstlane tells the compiler so (scalar descriptors)
     const int wi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = p.n_kv * REP;
+    const int log2_bs = p.log2_bs;
+    const uint32_t row_bytes = static_cast<uint32_t>(p.n_kv) * HD;   // bytes of one slot (all kv heads)
+    const int64_t blk_bytes = static_cast<int64_t>(row_bytes) << log2_bs;
+    const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
+    const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
+    const int bs_mask = (1 << log2_bs) - 1;
 
-    // first row to visit: the row holding tile u0, or the first of the empty rows sitting at u0
-    int lo = 0, hi = rows;               // last r with prefix[r] <= u0
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (prefix[mid] <= u0) lo = mid;
-        else hi = mid;
-    }
-    int r = lo;
-    if (prefix[r] == u0) {               // rewind over empty rows that also start at u0
-        int a = 0, b = r;
-        while (a < b) {
-            const int mid = (a + b) >> 1;
-            if (prefix[mid] < u0) a = mid + 1;
-            else b = mid;
+    // ---- first row to visit: the row holding tile u0, or the first empty row sitting at u0
+    int r_s;
+    {
+        int lo = 0, hi = rows;           // last r with prefix[r] <= u0
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (pfx(mid) <= u0) lo = mid;
+            else hi = mid;
         }
-        r = a;
-    }
-    for (; r < rows; ++r) {
-        const int64_t pr0 = prefix[r], pr1 = prefix[r + 1];
-        if (!(pr0 < u1 || (last_wg && pr0 == U))) break;
-        const int t = r / hg_count;
-        const int g = (r % hg_count) * wpg + wi;
-        if (pr1 == pr0) {                // empty context: zero output (reference: 0/0)
-#pragma unroll
-            for (int rr = 0; rr < REP; ++rr) {
-                uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD;
-                for (int d = lane; d < HD; d += 64) o[d] = 0;
+        r_s = lo;
+        if (pfx(r_s) == u0) {            // rewind over empty rows that also start at u0
+            int a = 0, b = r_s;
+            while (a < b) {
+                const int mid = (a + b) >> 1;
+                if (pfx(mid) < u0) a = mid + 1;
+                else b = mid;
             }
-            continue;
+            r_s = a;
         }
-        const int tb = static_cast<int>(max(u0, pr0) - pr0);
-        const int te = static_cast<int>(min(u1, pr1) - pr0);
-        if (tb >= te) continue;
-        float m[REP], l[REP], acc[REP][E];
-        scan_tiles<HD, REP, SM, ONE_BLOCK>(p, t, g, token_len(p, t), tb, te, m, l, acc);
-        if (grp != 0) continue;
-        if (tb == 0 && te == pr1 - pr0) {  // whole row: finish in place
+    }
+    // ---- empty rows of the range (kv_len <= 0): zero output (the reference would give 0/0)
+    for (int r = r_s; r < rows; ++r) {
+        const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
+        if (!(pr0 < u1 || (last_wg && pr0 == U))) break;
+        if (pr1 != pr0) continue;
+        const int t = r / hg_count, g = (r % hg_count) * wpg + wi;
+#pragma unroll
+        for (int rr = 0; rr < REP; ++rr) {
+            uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD;
+            for (int dd = lane; dd < HD; dd += 64) o[dd] = 0;
+        }
+    }
+
+    // ---- pieces: the non-empty rows of [u0, u1), in order
+    auto piece_from = [&](int r) -> Piece {
+        for (; r < rows; ++r) {
+            const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
+            if (pr0 >= u1) break;
+            if (pr1 == pr0) continue;
+            Piece pc;
+            pc.row = r;
+            pc.t = r / hg_count;
+            pc.g = (r % hg_count) * wpg + wi;
+            pc.kv_len = token_len_uniform(p, pc.t);
+            pc.lt = static_cast<int>(max(u0, pr0) - pr0);
+            pc.le = static_cast<int>(min(u1, pr1) - pr0);
+            pc.seq = max(ld_uniform(p.token_seq, pc.t), int64_t{0});
+            return pc;
+        }
+        Piece none;
+        none.row = -1;
+        none.t = 0;
+        none.g = wi;
+        none.kv_len = 1;
+        none.lt = 0;
+        none.le = 1;
+        none.seq = 0;
+        return none;
+    };
+
+    struct Tile {
+        VT k[kSteps], v[kSteps];
+        float ks[kSteps], vs[kSteps];
+    };
+    // Physical blocks of a tile: `lo` for its first 16 keys, `hi` for the last 16 (equal unless
+    // block_size == 16). Wave-uniform scalar loads, issued one tile ahead of the loads using them.
+    struct Phys {
+        int64_t lo, hi;
+    };
+    auto lookup = [&](const Piece& pc, int tile) -> Phys {
+        const int64_t seq = static_cast<int64_t>(uniform(static_cast<int>(pc.seq)));
+        const int64_t* table = p.block_tables + seq * p.table_width;
+        const int p0 = uniform(tile * kTileKeys);
+        const int64_t lo = max(ld_uniform(table, p0 >> log2_bs), int64_t{0});
+        if constexpr (ONE_BLOCK) return {lo, lo};
+        const int64_t hi = max(ld_uniform(table, uniform(min(p0 + kTileKeys / 2, pc.kv_len - 1) >> log2_bs)),
+                               int64_t{0});
+        return {lo, hi};
+    };
+    // Keys past kv_len (a row's last tile) are clamped to key kv_len-1: a valid, finite row whose
+    // score is masked. live = false (no work left): zero-size descriptors, no memory traffic.
+    auto load_tile = [&](const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
+        const int p0 = tile * kTileKeys;
+        const uint32_t lv = static_cast<uint32_t>(live);             // arithmetic, not a branch
+        const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
+        const uint32_t lane_col = pc.g * HD + sub * E;              // byte column inside a slot row
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const int64_t ph = (ONE_BLOCK || s < kSteps / 2) ? ph2.lo : ph2.hi;
+            const int pos = min(p0 + 8 * s + grp, pc.kv_len - 1);
+            const uint32_t in_blk = static_cast<uint32_t>(pos & bs_mask);
+            const uint32_t off = in_blk * row_bytes + lane_col;
+            tl.k[s] = buf_load<VT>(make_rsrc(p.k_cache + ph * blk_bytes, kv_rec), off);
+            tl.v[s] = buf_load<VT>(make_rsrc(p.v_cache + ph * blk_bytes, kv_rec), off);
+            if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
+                const int64_t sbase = (ph * p.n_kv + pc.g) << log2_bs;
+                tl.ks[s] = buf_load_f32(make_rsrc(p.k_scale + sbase, s_rec), in_blk * 4u);
+                tl.vs[s] = buf_load_f32(make_rsrc(p.v_scale + sbase, s_rec), in_blk * 4u);
+            } else {
+                tl.ks[s] = 1.f;
+                tl.vs[s] = 1.f;
+            }
+        }
+    };
+    // q slice for the REP heads of the piece's kv head, kept as raw bf16 pairs: the scores are
+    // bf16 x bf16 dot products (v_dot2c_f32_bf16) against K converted fp8 -> bf16, both exact, and
+    // scale*log2(e) [*k_scale] is applied to each score. The next piece's q is prefetched with its
+    // first tile.
+    const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? p.q_scale * p.k_scale[0] : p.q_scale;
+    constexpr int QW = E / 2;                       // 32-bit words of bf16 pairs per head per lane
+    // Issued in straight-line code every prefetch; `want` = false gives a zero-size descriptor
+    // (no traffic, qd = 0), so the wait counts before each compute stay exact.
+    auto load_q = [&](const Piece& pc, uint32_t (&qd)[REP][QW], bool want) {
+        const uint16_t* qh = p.q + ((int64_t)pc.t * H + pc.g * REP) * HD;     // REP heads, contiguous
+        const __amdgpu_buffer_rsrc_t qr = make_rsrc(qh, (REP * HD * 2) * static_cast<uint32_t>(want));
+#pragma unroll
+        for (int r = 0; r < REP; ++r)
+#pragma unroll
+            for (int c = 0; c < E / 8; ++c) {
+                const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(qr, (r * HD + sub * E + 8 * c) * 2, 0, 0);
+                qd[r][4 * c] = u[0];
+                qd[r][4 * c + 1] = u[1];
+                qd[r][4 * c + 2] = u[2];
+                qd[r][4 * c + 3] = u[3];
+            }
+    };
+    uint32_t qf[REP][QW], qn[REP][QW];
+    auto take_q = [&]() {
+#pragma unroll
+        for (int r = 0; r < REP; ++r)
+#pragma unroll
+            for (int i = 0; i < QW; ++i) qf[r][i] = qn[r][i];
+    };
+    // running max per key group; a finite floor so an all-masked group gives exp2(-inf) = 0
+    float m[REP], l[REP], acc[REP][E];
+    auto reset = [&]() {
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+            m[r] = kMinusHuge;
+            l[r] = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[r][e] = 0.f;
+        }
+    };
+    auto compute = [&](const Piece& pc, int tile, const Tile& tl) {
+        const int p0 = tile * kTileKeys;
+        float sc[REP][kSteps];
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            uint32_t kw[E / 4];
+            V::words(tl.k[s], kw);
+#pragma unroll
+            for (int r = 0; r < REP; ++r) sc[r][s] = 0.f;
+#pragma unroll
+            for (int j = 0; j < E / 4; ++j) {
+                const bf16x2_t k01 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kw[j], 1.0f, false);
+                const bf16x2_t k23 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(kw[j], 1.0f, true);
+#pragma unroll
+                for (int r = 0; r < REP; ++r) {
+                    sc[r][s] = __builtin_amdgcn_fdot2_f32_bf16(k01, __builtin_bit_cast(bf16x2_t, qf[r][2 * j]),
+                                                               sc[r][s], false);
+                    sc[r][s] = __builtin_amdgcn_fdot2_f32_bf16(k23, __builtin_bit_cast(bf16x2_t, qf[r][2 * j + 1]),
+                                                               sc[r][s], false);
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const bool valid = (p0 + 8 * s + grp) < pc.kv_len;
+            const float f = (SM == CVH_SCALE_PER_TOKEN_HEAD) ? tl.ks[s] * qsc : qsc;
+#pragma unroll
+            for (int r = 0; r < REP; ++r) {
+                const float dsum = group8_sum(sc[r][s]) * f;
+                sc[r][s] = valid ? dsum : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+            float mt = sc[r][0];
+#pragma unroll
+            for (int s = 1; s < kSteps; ++s) mt = fmaxf(mt, sc[r][s]);
+            const bool need = mt > m[r] + kRescaleThreshold;    // per key group
+            if (__builtin_amdgcn_ballot_w64(need) != 0) {      // wave-uniform; rare after a piece's first tile
+                const float mn = need ? mt : m[r];
+                const float c = __builtin_amdgcn_exp2f(m[r] - mn);
+                l[r] *= c;
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[r][e] *= c;
+                m[r] = mn;
+            }
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                const float pr = __builtin_amdgcn_exp2f(sc[r][s] - m[r]);
+                l[r] += pr;
+                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) sc[r][s] = pr * tl.vs[s];
+                else sc[r][s] = pr;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            float vf[E];
+            V::to_f32(tl.v[s], vf);
+#pragma unroll
+            for (int r = 0; r < REP; ++r) {
+                const float wgt = sc[r][s];
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[r][e] += wgt * vf[e];
+            }
+        }
+    };
+    // End of a piece: combine the 8 key groups (rescale each to the wave max, then sum) and
+    // write the finished row, or the partial of a cut row to slot 0 (holds u0) / 1 (holds u1-1).
+    auto finish = [&](const Piece& pc) {
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+            const float M = across_groups_max(m[r]);
+            const float c = __builtin_amdgcn_exp2f(m[r] - M);
+            m[r] = M;
+            l[r] = across_groups_sum(l[r] * c);   // l is uniform inside a group
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc[r][e] = across_groups_sum(acc[r][e] * c);
+        }
+        if (grp != 0) return;
+        const int64_t pr0 = pfx(pc.row), pr1 = pfx(pc.row + 1);
+        if (pc.lt == 0 && pc.le == pr1 - pr0) {
             const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
 #pragma unroll
-            for (int rr = 0; rr < REP; ++rr) {
-                const float f = vfin / l[rr];
-                uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD + sub * E;
+            for (int r = 0; r < REP; ++r) {
+                const float f = vfin / l[r];
+                uint16_t* o = p.out + ((int64_t)pc.t * H + pc.g * REP + r) * HD + sub * E;
 #pragma unroll
                 for (int c = 0; c < E / 8; ++c) {
                     uint32_t wd[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        wd[i] = f32_to_bf16_bits(acc[rr][c * 8 + 2 * i] * f) |
-                                (uint32_t(f32_to_bf16_bits(acc[rr][c * 8 + 2 * i + 1] * f)) << 16);
+                        wd[i] = f32_to_bf16_bits(acc[r][c * 8 + 2 * i] * f) |
+                                (uint32_t(f32_to_bf16_bits(acc[r][c * 8 + 2 * i + 1] * f)) << 16);
                     reinterpret_cast<uint4*>(o)[c] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
                 }
             }
-        } else {                          // cut row: partial to slot 0 (holds u0) or 1 (holds u1-1)
+        } else {
             const int slot = (pr0 <= u0) ? 0 : 1;
 #pragma unroll
-            for (int rr = 0; rr < REP; ++rr) {
-                const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP + rr;
+            for (int r = 0; r < REP; ++r) {
+                const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP + r;
                 float* pa = p.part_acc + idx * HD + sub * E;
 #pragma unroll
                 for (int c = 0; c < E / 4; ++c)
                     reinterpret_cast<float4*>(pa)[c] =
-                            make_float4(acc[rr][4 * c], acc[rr][4 * c + 1], acc[rr][4 * c + 2], acc[rr][4 * c + 3]);
-                if (sub == 0) reinterpret_cast<float2*>(p.part_ml)[idx] = make_float2(m[rr], l[rr]);
+                            make_float4(acc[r][4 * c], acc[r][4 * c + 1], acc[r][4 * c + 2], acc[r][4 * c + 3]);
+                if (sub == 0) reinterpret_cast<float2*>(p.part_ml)[idx] = make_float2(m[r], l[r]);
             }
+        }
+    };
+
+    // ---- one tile stream over all pieces, prefetching one tile ahead across piece boundaries
+    Piece pa_ = piece_from(r_s);
+    if (pa_.row < 0) return;
+    int ta_ = pa_.lt;
+    Tile A, B;
+    Piece pb_;
+    int tb_;
+    Piece lp = pa_;                      // load cursor (the tile after the newest buffered one)
+    int lt = ta_;
+    auto advance = [&]() {
+        if (lt + 1 < lp.le) ++lt;
+        else if (lp.row >= 0) {
+            lp = piece_from(lp.row + 1);
+            lt = lp.lt;
+        }
+    };
+    load_q(pa_, qn, true);
+    take_q();
+    reset();
+    load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
+    advance();
+    Phys ph = lookup(lp, lt);
+    for (;;) {
+        // prefetch into B, then compute A
+        pb_ = lp;
+        tb_ = lt;
+        const bool live_b = pb_.row >= 0;
+        load_q(pb_, qn, live_b && pb_.row != pa_.row);   // before the tile: its wait then spares the tile
+        load_tile(pb_, tb_, B, ph, live_b);
+        advance();
+        ph = lookup(lp, lt);
+        compute(pa_, ta_, A);
+        if (ta_ + 1 == pa_.le) {
+            finish(pa_);
+            if (!live_b) break;
+            reset();
+            take_q();
+        }
+        // prefetch into A, then compute B
+        pa_ = lp;
+        ta_ = lt;
+        const bool live_a = pa_.row >= 0;
+        load_q(pa_, qn, live_a && pa_.row != pb_.row);
+        load_tile(pa_, ta_, A, ph, live_a);
+        advance();
+        ph = lookup(lp, lt);
+        compute(pb_, tb_, B);
+        if (tb_ + 1 == pb_.le) {
+            finish(pb_);
+            if (!live_a) break;
+            reset();
+            take_q();
         }
     }
 }
