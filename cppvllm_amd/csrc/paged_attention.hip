@@ -48,7 +48,9 @@ constexpr int kTileKeys = 8 * kSteps;      // 32 keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: stale max tolerated up to p = 2^8
 constexpr float kMinusHuge = -1e30f;
-constexpr int kMaxRows = 16383;            // rows (tokens x head groups) per launch: LDS prefix
+constexpr int kMaxRows = 12287;            // rows (tokens x head groups) per launch: LDS prefix
+constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
+constexpr int kMaxQRows = 8;
 constexpr int kAutoPartitions = 512;       // MI355X: 256 CUs x 2 resident 4-wave workgroups
 
 // ---- buffer loads ------------------------------------------------------------------------------
@@ -174,6 +176,7 @@ struct Params {
     int num_tokens;
     int n_kv;
     int wpg;                 // kv heads (waves) per workgroup
+    int qrows;               // rows per workgroup whose q is staged in LDS by the prologue
     int log2_bs;
     float q_scale;           // softmax scale * log2(e)
 };
@@ -191,6 +194,16 @@ __device__ __forceinline__ int token_len_uniform(const Params& p, int t) {
     const int64_t cap = p.table_width << p.log2_bs;
     if (kv > cap) kv = cap;
     return kv > 0 ? static_cast<int>(kv) : 0;
+}
+
+// Dynamic LDS: row tile prefix (int [rows + 1]), then the q staging area
+// (bf16 [qrows][WPG][REP][HD]) on a 16-byte boundary.
+__host__ __device__ inline size_t lds_q_offset(int rows) {
+    return ((static_cast<size_t>(rows) + 1) * 4 + 15) & ~size_t{15};
+}
+inline int q_stage_rows(int wpg, int rep, int hd) {
+    const int per_row = wpg * rep * hd * 2;
+    return std::max(1, std::min(kMaxQRows, kQStageBytes / per_row));
 }
 
 // Exclusive prefix of row tile counts into LDS (prefix[0..rows]); all threads of the block.
@@ -304,8 +317,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
     }
 
     // ---- pieces: the non-empty rows of [u0, u1), in order
-    auto piece_from = [&](int r) -> Piece {
-        for (; r < rows; ++r) {
+    auto piece_from = [&](int r, int rlim) -> Piece {
+        for (; r < rlim; ++r) {
             const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
             if (pr0 >= u1) break;
             if (pr1 == pr0) continue;
@@ -376,32 +389,35 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
     };
     // q slice for the REP heads of the piece's kv head, kept as raw bf16 pairs: the scores are
     // bf16 x bf16 dot products (v_dot2c_f32_bf16) against K converted fp8 -> bf16, both exact, and
-    // scale*log2(e) [*k_scale] is applied to each score. The next piece's q is prefetched with its
-    // first tile.
+    // scale*log2(e) [*k_scale] is applied to each score. Rows are processed in batches of up to
+    // qrows rows whose q is first staged in LDS (each wave its own head), so starting a piece
+    // reads LDS and never waits behind the K/V loads in flight.
     const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? p.q_scale * p.k_scale[0] : p.q_scale;
     constexpr int QW = E / 2;                       // 32-bit words of bf16 pairs per head per lane
-    // Issued in straight-line code every prefetch; `want` = false gives a zero-size descriptor
-    // (no traffic, qd = 0), so the wait counts before each compute stay exact.
-    auto load_q = [&](const Piece& pc, uint32_t (&qd)[REP][QW], bool want) {
-        const uint16_t* qh = p.q + ((int64_t)pc.t * H + pc.g * REP) * HD;     // REP heads, contiguous
-        const __amdgpu_buffer_rsrc_t qr = make_rsrc(qh, (REP * HD * 2) * static_cast<uint32_t>(want));
+    uint16_t* q_lds = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(prefix) + lds_q_offset(rows));
+    int rb = r_s;                        // first row of the current batch of up to qrows rows
+    auto stage_q = [&](int rlim) {       // q of rows [rb, rlim) -> LDS, this wave's head
+        for (int r = rb; r < rlim; ++r) {
+            const int t = r / hg_count, g = (r % hg_count) * wpg + wi;
+            const uint16_t* src = p.q + ((int64_t)t * H + g * REP) * HD;
+            uint16_t* dst = q_lds + ((r - rb) * wpg + wi) * (REP * HD);
+            for (int o = lane * 8; o < REP * HD; o += 64 * 8)
+                *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(src + o);
+        }
+    };
+    uint32_t qf[REP][QW];
+    auto take_q = [&](const Piece& pc) {
+        const uint16_t* src = q_lds + ((pc.row - rb) * wpg + wi) * (REP * HD);
 #pragma unroll
         for (int r = 0; r < REP; ++r)
 #pragma unroll
             for (int c = 0; c < E / 8; ++c) {
-                const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(qr, (r * HD + sub * E + 8 * c) * 2, 0, 0);
-                qd[r][4 * c] = u[0];
-                qd[r][4 * c + 1] = u[1];
-                qd[r][4 * c + 2] = u[2];
-                qd[r][4 * c + 3] = u[3];
+                const uint4 u = *reinterpret_cast<const uint4*>(src + r * HD + sub * E + 8 * c);
+                qf[r][4 * c] = u.x;
+                qf[r][4 * c + 1] = u.y;
+                qf[r][4 * c + 2] = u.z;
+                qf[r][4 * c + 3] = u.w;
             }
-    };
-    uint32_t qf[REP][QW], qn[REP][QW];
-    auto take_q = [&]() {
-#pragma unroll
-        for (int r = 0; r < REP; ++r)
-#pragma unroll
-            for (int i = 0; i < QW; ++i) qf[r][i] = qn[r][i];
     };
     // running max per key group; a finite floor so an all-masked group gives exp2(-inf) = 0
     float m[REP], l[REP], acc[REP][E];
@@ -525,59 +541,76 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
         }
     };
 
-    // ---- one tile stream over all pieces, prefetching one tile ahead across piece boundaries
-    Piece pa_ = piece_from(r_s);
-    if (pa_.row < 0) return;
-    int ta_ = pa_.lt;
-    Tile A, B;
-    Piece pb_;
-    int tb_;
-    Piece lp = pa_;                      // load cursor (the tile after the newest buffered one)
-    int lt = ta_;
-    auto advance = [&]() {
-        if (lt + 1 < lp.le) ++lt;
-        else if (lp.row >= 0) {
-            lp = piece_from(lp.row + 1);
-            lt = lp.lt;
-        }
-    };
-    load_q(pa_, qn, true);
-    take_q();
-    reset();
-    load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
-    advance();
-    Phys ph = lookup(lp, lt);
+    // ---- per batch: one tile stream over its pieces, two tiles in flight ahead of the one being
+    // computed (register triple buffer, unrolled by three so no tile is copied between buffers)
     for (;;) {
-        // prefetch into B, then compute A
-        pb_ = lp;
-        tb_ = lt;
-        const bool live_b = pb_.row >= 0;
-        load_q(pb_, qn, live_b && pb_.row != pa_.row);   // before the tile: its wait then spares the tile
-        load_tile(pb_, tb_, B, ph, live_b);
-        advance();
-        ph = lookup(lp, lt);
-        compute(pa_, ta_, A);
-        if (ta_ + 1 == pa_.le) {
-            finish(pa_);
-            if (!live_b) break;
+        if (rb >= rows || pfx(rb) >= u1) return;
+        const int rlim = min(rows, rb + p.qrows);
+        stage_q(rlim);
+        Piece pa_ = piece_from(rb, rlim);
+        if (pa_.row >= 0) {
+            int ta_ = pa_.lt;
+            Tile A, B, C;
+            Piece pb_, pc_;
+            int tb_, tc_;
+            Piece lp = pa_;              // load cursor (the tile after the newest buffered one)
+            int lt = ta_;
+            auto advance = [&]() {
+                if (lt + 1 < lp.le) ++lt;
+                else if (lp.row >= 0) {
+                    lp = piece_from(lp.row + 1, rlim);
+                    lt = lp.lt;
+                }
+            };
+            take_q(pa_);
             reset();
-            take_q();
+            load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
+            advance();
+            pb_ = lp;
+            tb_ = lt;
+            load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
+            advance();
+            Phys ph = lookup(lp, lt);
+            for (;;) {
+                pc_ = lp;
+                tc_ = lt;
+                load_tile(pc_, tc_, C, ph, pc_.row >= 0);
+                advance();
+                ph = lookup(lp, lt);
+                compute(pa_, ta_, A);
+                if (ta_ + 1 == pa_.le) {
+                    finish(pa_);
+                    if (pb_.row < 0) break;
+                    reset();
+                    take_q(pb_);
+                }
+                pa_ = lp;
+                ta_ = lt;
+                load_tile(pa_, ta_, A, ph, pa_.row >= 0);
+                advance();
+                ph = lookup(lp, lt);
+                compute(pb_, tb_, B);
+                if (tb_ + 1 == pb_.le) {
+                    finish(pb_);
+                    if (pc_.row < 0) break;
+                    reset();
+                    take_q(pc_);
+                }
+                pb_ = lp;
+                tb_ = lt;
+                load_tile(pb_, tb_, B, ph, pb_.row >= 0);
+                advance();
+                ph = lookup(lp, lt);
+                compute(pc_, tc_, C);
+                if (tc_ + 1 == pc_.le) {
+                    finish(pc_);
+                    if (pa_.row < 0) break;
+                    reset();
+                    take_q(pa_);
+                }
+            }
         }
-        // prefetch into A, then compute B
-        pa_ = lp;
-        ta_ = lt;
-        const bool live_a = pa_.row >= 0;
-        load_q(pa_, qn, live_a && pa_.row != pb_.row);
-        load_tile(pa_, ta_, A, ph, live_a);
-        advance();
-        ph = lookup(lp, lt);
-        compute(pb_, tb_, B);
-        if (tb_ + 1 == pb_.le) {
-            finish(pb_);
-            if (!live_a) break;
-            reset();
-            take_q();
-        }
+        rb = rlim;
     }
 }
 
@@ -742,6 +775,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     p.num_tokens = static_cast<int>(num_tokens);
     p.n_kv = n_kv_heads;
     p.wpg = wpg;
+    p.qrows = q_stage_rows(wpg, rep, head_dim);
     p.log2_bs = lg;
     // The softmax scale is folded into q with log2(e) (base-2 softmax); a per-tensor K scale is a
     // device float, so the kernel folds it into q after reading it.
@@ -749,7 +783,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
 
     auto s = reinterpret_cast<hipStream_t>(stream);
     if (phase & kPhaseDecode) {
-        const size_t lds = static_cast<size_t>(rows + 1) * sizeof(int);
+        const size_t lds = lds_q_offset(static_cast<int>(rows)) + static_cast<size_t>(p.qrows) * wpg * rep * head_dim * 2;
         const bool one_block = (1 << lg) >= kTileKeys;
         bool ok;
         if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
