@@ -48,10 +48,10 @@ constexpr int kTileKeys = 8 * kSteps;      // 32 keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: stale max tolerated up to p = 2^8
 constexpr float kMinusHuge = -1e30f;
-constexpr int kMaxRows = 12287;            // rows (tokens x head groups) per launch: LDS prefix
+constexpr int kMaxRows = 8192;             // rows (tokens x head groups) per launch: LDS prefix
 constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
 constexpr int kMaxQRows = 8;
-constexpr int kAutoPartitions = 512;       // MI355X: 256 CUs x 2 resident 4-wave workgroups
+constexpr int kResidentWaves = 2048;       // MI355X: 256 CUs x 4 SIMDs x 2 waves (<= 256 VGPRs each)
 
 // ---- buffer loads ------------------------------------------------------------------------------
 // K/V rows and scales go through raw buffer loads: the descriptor's record count bounds every
@@ -188,33 +188,36 @@ __device__ __forceinline__ int token_len(const Params& p, int t) {
     if (kv > cap) kv = cap;
     return kv > 0 ? static_cast<int>(kv) : 0;
 }
-// The same for a wave-uniform t (scalar load).
-__device__ __forceinline__ int token_len_uniform(const Params& p, int t) {
-    int64_t kv = ld_uniform(p.token_kv_len, t);
-    const int64_t cap = p.table_width << p.log2_bs;
-    if (kv > cap) kv = cap;
-    return kv > 0 ? static_cast<int>(kv) : 0;
-}
 
-// Dynamic LDS: row tile prefix (int [rows + 1]), then the q staging area
-// (bf16 [qrows][WPG][REP][HD]) on a 16-byte boundary.
-__host__ __device__ inline size_t lds_q_offset(int rows) {
-    return ((static_cast<size_t>(rows) + 1) * 4 + 15) & ~size_t{15};
+// Dynamic LDS: row tile prefix (int [rows + 1]); per-token (clamped kv_len, block-table row)
+// (int2 [T]); the q staging area (bf16 [qrows][WPG][REP][HD]) on a 16-byte boundary.
+__host__ __device__ inline size_t lds_tok_offset(int rows) {
+    return ((static_cast<size_t>(rows) + 1) * 4 + 7) & ~size_t{7};
+}
+__host__ __device__ inline size_t lds_q_offset(int rows, int tokens) {
+    return (lds_tok_offset(rows) + static_cast<size_t>(tokens) * 8 + 15) & ~size_t{15};
 }
 inline int q_stage_rows(int wpg, int rep, int hd) {
     const int per_row = wpg * rep * hd * 2;
     return std::max(1, std::min(kMaxQRows, kQStageBytes / per_row));
 }
 
-// Exclusive prefix of row tile counts into LDS (prefix[0..rows]); all threads of the block.
-__device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int hg_count, int* prefix) {
+// Token metadata and the exclusive prefix of row tile counts into LDS (prefix[0..rows]); all
+// threads of the block. kv_len and the block-table row of every token are fetched together (one
+// memory round trip), so later lookups of a piece's token read LDS.
+__device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int hg_count, int* prefix, int2* tok) {
     __shared__ int wave_tot[16];
     const int nthreads = blockDim.x;
     const int tid = threadIdx.x;
+    for (int t = tid; t < p.num_tokens; t += nthreads) {
+        const int64_t sq = p.token_seq[t];
+        tok[t] = make_int2(token_len(p, t), static_cast<int>(sq > 0 ? sq : 0));
+    }
+    __syncthreads();
     const int per = (rows + nthreads - 1) / nthreads;
     const int beg = min(rows, tid * per), end = min(rows, beg + per);
     int s = 0;
-    for (int r = beg; r < end; ++r) s += (token_len(p, r / hg_count) + kTileKeys - 1) / kTileKeys;
+    for (int r = beg; r < end; ++r) s += (tok[r / hg_count].x + kTileKeys - 1) / kTileKeys;
     // inclusive scan over the wave
     const int lane = tid & 63, wv = tid >> 6;
     int incl = s;
@@ -230,7 +233,7 @@ __device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int 
     int run = off + incl - s;            // exclusive prefix of this thread's chunk
     for (int r = beg; r < end; ++r) {
         prefix[r] = run;
-        run += (token_len(p, r / hg_count) + kTileKeys - 1) / kTileKeys;
+        run += (tok[r / hg_count].x + kTileKeys - 1) / kTileKeys;
     }
     if (tid == nthreads - 1) {
         int tot = 0;
@@ -249,7 +252,7 @@ struct Piece {
 };
 
 template <int HD, int REP, int SM, bool ONE_BLOCK>
-__global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
+__global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     using V = KvVec<HD>;
     using VT = typename V::T;
     constexpr int E = V::kElems;
@@ -257,7 +260,8 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
     const int wpg = p.wpg;
     const int hg_count = p.n_kv / wpg;
     const int rows = p.num_tokens * hg_count;
-    build_row_prefix(p, rows, hg_count, prefix);
+    int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows));
+    build_row_prefix(p, rows, hg_count, prefix, tok);
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
 
@@ -326,10 +330,11 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
             pc.row = r;
             pc.t = r / hg_count;
             pc.g = (r % hg_count) * wpg + wi;
-            pc.kv_len = token_len_uniform(p, pc.t);
+            const int2 tm = tok[pc.t];
+            pc.kv_len = uniform(tm.x);
             pc.lt = static_cast<int>(max(u0, pr0) - pr0);
             pc.le = static_cast<int>(min(u1, pr1) - pr0);
-            pc.seq = max(ld_uniform(p.token_seq, pc.t), int64_t{0});
+            pc.seq = uniform(tm.y);
             return pc;
         }
         Piece none;
@@ -394,7 +399,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
     // reads LDS and never waits behind the K/V loads in flight.
     const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? p.q_scale * p.k_scale[0] : p.q_scale;
     constexpr int QW = E / 2;                       // 32-bit words of bf16 pairs per head per lane
-    uint16_t* q_lds = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(prefix) + lds_q_offset(rows));
+    uint16_t* q_lds = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens));
     int rb = r_s;                        // first row of the current batch of up to qrows rows
     auto stage_q = [&](int rlim) {       // q of rows [rb, rlim) -> LDS, this wave's head
         for (int r = rb; r < rlim; ++r) {
@@ -546,7 +551,6 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
     for (;;) {
         if (rb >= rows || pfx(rb) >= u1) return;
         const int rlim = min(rows, rb + p.qrows);
-        stage_q(rlim);
         Piece pa_ = piece_from(rb, rlim);
         if (pa_.row >= 0) {
             int ta_ = pa_.lt;
@@ -562,8 +566,7 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
                     lt = lp.lt;
                 }
             };
-            take_q(pa_);
-            reset();
+            // the first two tiles are in flight before q is staged: their latency covers it
             load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
             advance();
             pb_ = lp;
@@ -571,6 +574,9 @@ __global__ __launch_bounds__(256, 2) void paged_decode_kernel(Params p) {
             load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
             advance();
             Phys ph = lookup(lp, lt);
+            stage_q(rlim);
+            take_q(pa_);
+            reset();
             for (;;) {
                 pc_ = lp;
                 tc_ = lt;
@@ -677,7 +683,9 @@ int ilog2_pow2(int64_t v) {
     return l;
 }
 
-int waves_per_group(int n_kv) { return (n_kv % 4 == 0) ? 4 : (n_kv % 2 == 0) ? 2 : 1; }
+// One wave per kv head of a row group. Eight kv heads share a workgroup when they can: a tile is
+// then whole 1 KiB slot rows (all heads of 32 keys), contiguous in HBM.
+int waves_per_group(int n_kv) { return (n_kv % 8 == 0) ? 8 : (n_kv % 4 == 0) ? 4 : (n_kv % 2 == 0) ? 2 : 1; }
 
 // Upper bound of the tile count U, from what the host knows (widths, not lengths).
 int64_t tile_bound(int64_t T, int n_kv, int64_t table_width, int block_size) {
@@ -688,7 +696,7 @@ int64_t tile_bound(int64_t T, int n_kv, int64_t table_width, int block_size) {
 int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
     // one partition per resident workgroup slot, but never less than 2 tiles per partition
     const int64_t b = (tile_bound(T, n_kv, table_width, block_size) + 1) / 2;
-    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kAutoPartitions, b)));
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kResidentWaves / waves_per_group(n_kv), b)));
 }
 
 // Workspace: prefix int32 [rows + 1] | part_acc float [G][2][WPG][REP][HD] | part_ml float2 [...]
@@ -710,12 +718,20 @@ Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
 
 enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3 };
 
+template <typename K>
+void launch_with_lds(K kernel, int G, int threads, size_t lds, hipStream_t s, const Params& p) {
+    if (lds > 65536)   // large token counts: opt in to more than 64 KiB of dynamic LDS
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds));
+    kernel<<<dim3(G), threads, lds, s>>>(p);
+}
+
 template <int HD, int REP, int SM>
 void launch_decode(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
     if (one_block)
-        paged_decode_kernel<HD, REP, SM, true><<<dim3(G), threads, lds, s>>>(p);
+        launch_with_lds(paged_decode_kernel<HD, REP, SM, true>, G, threads, lds, s, p);
     else
-        paged_decode_kernel<HD, REP, SM, false><<<dim3(G), threads, lds, s>>>(p);
+        launch_with_lds(paged_decode_kernel<HD, REP, SM, false>, G, threads, lds, s, p);
 }
 
 template <int HD, int SM>
@@ -783,7 +799,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
 
     auto s = reinterpret_cast<hipStream_t>(stream);
     if (phase & kPhaseDecode) {
-        const size_t lds = lds_q_offset(static_cast<int>(rows)) + static_cast<size_t>(p.qrows) * wpg * rep * head_dim * 2;
+        const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens)) +
+                           static_cast<size_t>(p.qrows) * wpg * rep * head_dim * 2;
         const bool one_block = (1 << lg) >= kTileKeys;
         bool ok;
         if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)

@@ -110,6 +110,17 @@ def test_chunked_prefill_rows(orc):
     assert_close_bf16(run_gpu(dev(b)), run_oracle(orc, b))
 
 
+def test_max_rows_per_launch(orc):
+    # 8192 query tokens x 8 kv heads = 8192 rows, the per-launch limit (LDS above 64 KiB);
+    # the oracle checks a seeded sample of 192 rows
+    say("max rows per launch: 8 seqs x 1024 chunked-prefill tokens")
+    b = synth(41, [1024, 1100, 1500, 2000, 1024, 1300, 1700, 1900], 256, queries_per_seq=1024)
+    assert b["q"].shape[0] == 8192
+    got = run_gpu(dev(b))
+    rows = sorted(np.random.default_rng(41).choice(8192, 192, replace=False).tolist())
+    assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
+
+
 def test_empty_context_rows_are_zero(orc):
     say("kv_len 0 rows")
     b = synth(5, [100, 50], 16)

@@ -43,8 +43,14 @@ def test_argument_validation_without_device():
     # workspace missing
     assert lib.cvh_paged_attention_fp8_ex(*args, 8, p, p, 4, 16, 8, 128, 16, 0, 0.1, 64, None, 0,
                                           None) == _lib.CVH_ERR_WORKSPACE
-    # too many rows for one launch
+    # too many rows for one launch: 8192 tokens at <= 8 kv heads, 4096 at 16
     assert lib.cvh_paged_attention_fp8(*args, 1, p, p, 20000, 16, 8, 128, 16, 0, 0.1, p, 1 << 30,
+                                       None) == unsup
+    assert lib.cvh_paged_attention_fp8(*args, 1, p, p, 8193, 16, 8, 128, 16, 0, 0.1, p, 1 << 30,
+                                       None) == unsup
+    assert lib.cvh_paged_attention_fp8(*args, 1, p, p, 8193, 4, 4, 128, 16, 0, 0.1, p, 1 << 30,
+                                       None) == unsup
+    assert lib.cvh_paged_attention_fp8(*args, 1, p, p, 4097, 16, 16, 128, 16, 0, 0.1, p, 1 << 30,
                                        None) == unsup
     assert lib.cvh_rms_norm(p, p, p, 3, 1020, 1e-6, 0, None) == unsup
     assert lib.cvh_rms_norm(p, p, p, 3, 1024, 1e-6, 7, None) == unsup
@@ -54,15 +60,16 @@ def test_argument_validation_without_device():
 
 def test_partition_policy_and_workspace_sizes():
     lib = _lib.lib()
-    # headline decode (256 tokens, 8 kv heads = 2 row groups, 8 x 256-token blocks): 512 partitions
-    assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 512
-    rows, slots = 256 * 2, 512 * 2 * 8     # [G][2][WPG*REP] partial slots
+    # headline decode (256 tokens, 8 kv heads = one 8-wave row group, 8 x 256-token blocks):
+    # 256 partitions (2048 resident waves / 8)
+    assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 256
+    rows, slots = 256, 256 * 2 * 16     # [G][2][WPG*REP] partial slots
     r256 = lambda v: (v + 255) // 256 * 256
     want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4)
     assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == want
     # small batches: never less than two tiles per partition
     assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
-    assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 8 * 2 * 32 // 2
+    assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 8 * 32 // 2
     assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 8, 16, -1) == 0
 
 
