@@ -626,7 +626,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 // thread i handles query head i / (HD/4) of the row and 4 consecutive dims; the pieces are
 // combined in one online pass (running max), so their loads are independent of each other.
 template <int HD, int SM>
-__global__ __launch_bounds__(256) void paged_merge_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
+__global__ __launch_bounds__(512) void paged_merge_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
                                                           const float* __restrict__ part_ml,
                                                           const int* __restrict__ prefix,
                                                           const float* __restrict__ v_scale, int num_tokens, int n_kv,
@@ -815,20 +815,22 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     }
     if ((phase & kPhaseMerge) && G > 1) {
         const dim3 mgrid(static_cast<unsigned>(rows));
+        // one thread per 4 output dims of the row's wpg*rep heads, up to 512 (more heads loop)
+        const int mthreads = std::min(512, wpg * rep * head_dim / 4);
         const int nt = static_cast<int>(num_tokens);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 256, 0, s>>>(
+                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
             else
-                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, 256, 0, s>>>(
+                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, mthreads, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
         } else {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, 256, 0, s>>>(
+                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
             else
-                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, 256, 0, s>>>(
+                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, mthreads, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
         }
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
