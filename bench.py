@@ -83,6 +83,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--partitions", type=int, default=0, help="work partitions (0 = automatic)")
     ap.add_argument("--eager", action="store_true", help="launch eagerly instead of replaying HIP graphs")
+    ap.add_argument("--unplanned", action="store_true",
+                    help="no per-step plan: every layer's launch derives its work layout itself")
     ap.add_argument("--config", type=int, default=3, choices=(3, 4),
                     help="3: 256 seqs, ctx U(100,1024)+U(0,1024) (headline); 4: 64 seqs, ctx log-U(4k,32k)")
     ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
@@ -128,8 +130,10 @@ def main():
     ws = torch.zeros(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
     out = torch.empty_like(b["q"])
     layer_ptrs = [tuple(x.data_ptr() for x in lay) for lay in layers]
-    # the op = decode kernel (split phase) + merge of cut rows (merge phase)
-    split_fn = lib.cvh_paged_attention_fp8_split_phase
+    # the op = decode kernel (split phase) + merge of cut rows (merge phase); by default a plan of
+    # the step's layout is built once per step and read by every layer's decode launch
+    planned = not args.unplanned
+    split_fn = lib.cvh_paged_attention_fp8_planned_split_phase if planned else lib.cvh_paged_attention_fp8_split_phase
     merge_fn = lib.cvh_paged_attention_fp8_merge_phase
 
     def launch(fn, lp):
@@ -140,12 +144,22 @@ def main():
         if code:
             raise _lib.CvhError("paged_attention_fp8", code)
 
-    def step():                   # one decode step: 28 layers, each decode + merge
+    def plan():
+        sp = torch.cuda.current_stream(dev).cuda_stream
+        code = lib.cvh_paged_attention_plan(b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(),
+                                            b["token_kv_len"].data_ptr(), T, H, KV, HD, BS, args.partitions,
+                                            ws.data_ptr(), ws_bytes, sp)
+        if code:
+            raise _lib.CvhError("paged_attention_plan", code)
+
+    def step():                   # one decode step: (plan), then 28 layers, each decode + merge
+        if planned:
+            plan()
         for lp in layer_ptrs:
             launch(split_fn, lp)
             launch(merge_fn, lp)
 
-    def decode_only():            # the dominant kernel alone, 28 launches back to back
+    def decode_only():            # the dominant kernel alone, 28 launches back to back (plan left by step())
         for lp in layer_ptrs:
             launch(split_fn, lp)
 
@@ -212,11 +226,13 @@ def main():
             if args.partitions == 0 else args.partitions,
             "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "launch": "eager" if args.eager else "hip_graph",
+            "plan": "once per step (cvh_paged_attention_plan), read by all layers" if planned else "none",
             "op_us_per_layer": round(total_ms * 1e3 / (args.steps * len(layer_ptrs)), 2),
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "paged_decode_kernel (split phase; graph of 28 back-to-back launches)",
+                     "kernel": "paged_decode_kernel (%s split phase; graph of 28 back-to-back launches)"
+                               % ("planned" if planned else "unplanned"),
                      "avg_launch_us": round(avg_layer_ms * 1e3, 2)},
     }
     if not args.no_cpu:

@@ -38,6 +38,11 @@ SIGNATURES = {
                                                   i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_merge_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32,
                                                   i32, f64, i32, vp, sz, vp]),
+    "cvh_paged_attention_plan": (i32, [vp, i64, vp, vp, i64, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_planned": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
+                                              f64, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_planned_split_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32,
+                                                          i32, i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_workspace_bytes": (sz, [i64, i32, i32, i32, i64, i32, i32]),
     "cvh_paged_attention_partitions": (i32, [i64, i32, i64, i32]),
     "cvh_rms_norm": (i32, [vp, vp, vp, i64, i32, f64, i32, vp]),

@@ -51,6 +51,7 @@ constexpr float kMinusHuge = -1e30f;
 constexpr int kMaxRows = 8192;             // rows (tokens x head groups) per launch: LDS prefix
 constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
 constexpr int kMaxQRows = 8;
+constexpr int kPreQRows = 4;               // q rows a planned launch fetches ahead of its first tiles
 constexpr int kResidentWaves = 2048;       // MI355X: 256 CUs x 4 SIMDs x 2 waves (<= 256 VGPRs each)
 
 // ---- buffer loads ------------------------------------------------------------------------------
@@ -159,8 +160,19 @@ template <typename T> __device__ __forceinline__ T ld_uniform(const T* ptr, int6
     return ((cptr)(uintptr_t)ptr)[i];
 }
 
+// Per-workgroup start of the decode stream, written by the plan kernel once per batch layout
+// (shared by every layer of a step): the first piece of the workgroup's first batch of rows and
+// the physical blocks of its first two tiles, so a planned launch issues them before anything
+// else. row < 0: no preload.
+struct PlanRec {
+    int row, lt, le, kv_len, seq, b_ok, r_s, pad;
+    int64_t a_lo, a_hi, b_lo, b_hi;
+};
+
 struct Params {
     uint16_t* out;
+    const PlanRec* plan;     // [G] (planned launches)
+    int2* plan_tok;          // [T] (kv_len, block-table row) per token, written by the plan kernel
     float* part_acc;         // [G][2][WPG][REP][HD]
     float* part_ml;          // [G][2][WPG][REP][2]
     int* prefix_out;         // [rows + 1] row tile prefix, written by workgroup 0 for the merge
@@ -243,6 +255,28 @@ __device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int 
     __syncthreads();
 }
 
+// First row a workgroup visits for tile range [u0, ...): the row holding tile u0, or the first
+// empty row sitting at u0 (so empty rows at a range boundary get zeroed exactly once).
+template <typename F> __device__ __forceinline__ int first_row(F pfx, int rows, int64_t u0) {
+    int lo = 0, hi = rows;               // last r with prefix[r] <= u0
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pfx(mid) <= u0) lo = mid;
+        else hi = mid;
+    }
+    int r = lo;
+    if (pfx(r) == u0) {                  // rewind over empty rows that also start at u0
+        int a = 0, b = r;
+        while (a < b) {
+            const int mid = (a + b) >> 1;
+            if (pfx(mid) < u0) a = mid + 1;
+            else b = mid;
+        }
+        r = a;
+    }
+    return r;
+}
+
 // One piece of work of a workgroup: tiles [lt, le) of row `row` (token t, kv head g of this wave).
 // row < 0 marks "no more work" (its other fields are safe dummies: loads made for it use zero-size
 // descriptors, and its table lookups stay inside block-table row 0).
@@ -251,7 +285,7 @@ struct Piece {
     int64_t seq;   // block-table row of token t
 };
 
-template <int HD, int REP, int SM, bool ONE_BLOCK>
+template <int HD, int REP, int SM, bool ONE_BLOCK, bool PLANNED>
 __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     using V = KvVec<HD>;
     using VT = typename V::T;
@@ -261,18 +295,11 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const int hg_count = p.n_kv / wpg;
     const int rows = p.num_tokens * hg_count;
     int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows));
-    build_row_prefix(p, rows, hg_count, prefix, tok);
-    if (blockIdx.x == 0)
-        for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
-
-    // prefix values are the same for every lane; uniform() makes that visible to the compiler so
+    // values that are the same for every lane; uniform() makes that visible to the compiler so
     // all the piece bookkeeping below stays in scalar registers
     auto uniform = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
-    auto pfx = [&](int i) { return uniform(prefix[i]); };
-    const int64_t U = pfx(rows);
     const int64_t G = gridDim.x;
     const int w = blockIdx.x;
-    const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
     const bool last_wg = (w == G - 1);
     const int lane = threadIdx.x & 63;
     const int grp = lane >> 3;
@@ -286,67 +313,6 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
     const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
     const int bs_mask = (1 << log2_bs) - 1;
-
-    // ---- first row to visit: the row holding tile u0, or the first empty row sitting at u0
-    int r_s;
-    {
-        int lo = 0, hi = rows;           // last r with prefix[r] <= u0
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (pfx(mid) <= u0) lo = mid;
-            else hi = mid;
-        }
-        r_s = lo;
-        if (pfx(r_s) == u0) {            // rewind over empty rows that also start at u0
-            int a = 0, b = r_s;
-            while (a < b) {
-                const int mid = (a + b) >> 1;
-                if (pfx(mid) < u0) a = mid + 1;
-                else b = mid;
-            }
-            r_s = a;
-        }
-    }
-    // ---- empty rows of the range (kv_len <= 0): zero output (the reference would give 0/0)
-    for (int r = r_s; r < rows; ++r) {
-        const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
-        if (!(pr0 < u1 || (last_wg && pr0 == U))) break;
-        if (pr1 != pr0) continue;
-        const int t = r / hg_count, g = (r % hg_count) * wpg + wi;
-#pragma unroll
-        for (int rr = 0; rr < REP; ++rr) {
-            uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD;
-            for (int dd = lane; dd < HD; dd += 64) o[dd] = 0;
-        }
-    }
-
-    // ---- pieces: the non-empty rows of [u0, u1), in order
-    auto piece_from = [&](int r, int rlim) -> Piece {
-        for (; r < rlim; ++r) {
-            const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
-            if (pr0 >= u1) break;
-            if (pr1 == pr0) continue;
-            Piece pc;
-            pc.row = r;
-            pc.t = r / hg_count;
-            pc.g = (r % hg_count) * wpg + wi;
-            const int2 tm = tok[pc.t];
-            pc.kv_len = uniform(tm.x);
-            pc.lt = static_cast<int>(max(u0, pr0) - pr0);
-            pc.le = static_cast<int>(min(u1, pr1) - pr0);
-            pc.seq = uniform(tm.y);
-            return pc;
-        }
-        Piece none;
-        none.row = -1;
-        none.t = 0;
-        none.g = wi;
-        none.kv_len = 1;
-        none.lt = 0;
-        none.le = 1;
-        none.seq = 0;
-        return none;
-    };
 
     struct Tile {
         VT k[kSteps], v[kSteps];
@@ -392,6 +358,124 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             }
         }
     };
+
+    Tile A, B, C;
+    // A planned launch starts its first two K/V tiles from the plan record before it builds
+    // anything, then copies the prefix and token metadata of the plan into LDS; otherwise the
+    // workgroup derives them from token_kv_len itself (one memory round trip more, then the
+    // block-table round trip before its first K/V load).
+    bool preA = false, preB = false, preQ = false;
+    int plan_row = -1, plan_lt = 0, plan_rs = -1;
+    char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens);
+    constexpr int QB = REP * HD * 2;                 // bytes of one row's q slice for one wave
+    constexpr int QL = (QB + 1023) / 1024;           // 16-byte loads per lane per row
+    if constexpr (PLANNED) {
+        // Everything the prologue waits for (q of the first rows, prefix, token metadata) is
+        // requested before the first two tiles, so the in-order vmcnt wait for it leaves the
+        // tiles in flight. Out-of-range entries use zero-size descriptors: straight-line code.
+        const PlanRec* rp = p.plan + w;
+        plan_row = ld_uniform(&rp->row, 0);
+        plan_rs = ld_uniform(&rp->r_s, 0);
+        uint4 qv[kPreQRows][QL];
+#pragma unroll
+        for (int r = 0; r < kPreQRows; ++r) {
+            const bool live = r < p.qrows && plan_rs + r < rows;
+            const int rr = live ? plan_rs + r : 0;
+            const int t = rr / hg_count, g = (rr % hg_count) * wpg + wi;
+            const auto rs = make_rsrc(p.q + (static_cast<int64_t>(t) * H + g * REP) * HD, live ? QB : 0);
+#pragma unroll
+            for (int j = 0; j < QL; ++j) qv[r][j] = buf_load<uint4>(rs, lane * 16 + j * 1024);
+        }
+        const int bd = blockDim.x, tid = threadIdx.x;
+        const auto pre_rs = make_rsrc(p.prefix_out, (rows + 1) * 4);
+        const auto tok_rs = make_rsrc(p.plan_tok, p.num_tokens * 8);
+        const int pv0 = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(pre_rs, tid * 4, 0, 0));
+        const int pv1 = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(pre_rs, (tid + bd) * 4, 0, 0));
+        const u32x2_t tv0 = __builtin_amdgcn_raw_buffer_load_b64(tok_rs, tid * 8, 0, 0);
+        const u32x2_t tv1 = __builtin_amdgcn_raw_buffer_load_b64(tok_rs, (tid + bd) * 8, 0, 0);
+        {
+            const bool live = plan_row >= 0;
+            Piece pc;
+            pc.row = live ? plan_row : 0;
+            pc.t = pc.row / hg_count;
+            pc.g = (pc.row % hg_count) * wpg + wi;
+            plan_lt = ld_uniform(&rp->lt, 0);
+            pc.lt = plan_lt;
+            pc.le = ld_uniform(&rp->le, 0);
+            pc.kv_len = live ? ld_uniform(&rp->kv_len, 0) : 1;
+            pc.seq = ld_uniform(&rp->seq, 0);
+            const bool b_ok = live && ld_uniform(&rp->b_ok, 0) != 0;
+            load_tile(pc, plan_lt, A, {ld_uniform(&rp->a_lo, 0), ld_uniform(&rp->a_hi, 0)}, live);
+            load_tile(pc, plan_lt + 1, B, {ld_uniform(&rp->b_lo, 0), ld_uniform(&rp->b_hi, 0)}, b_ok);
+            preA = live;
+            preB = b_ok;
+        }
+#pragma unroll
+        for (int r = 0; r < kPreQRows; ++r)
+#pragma unroll
+            for (int j = 0; j < QL; ++j)
+                if (r < p.qrows && lane * 16 + j * 1024 < QB)
+                    *reinterpret_cast<uint4*>(q_lds_b + (r * wpg + wi) * QB + lane * 16 + j * 1024) = qv[r][j];
+        if (tid <= rows) prefix[tid] = pv0;
+        if (tid + bd <= rows) prefix[tid + bd] = pv1;
+        if (tid < p.num_tokens) tok[tid] = make_int2(static_cast<int>(tv0[0]), static_cast<int>(tv0[1]));
+        if (tid + bd < p.num_tokens) tok[tid + bd] = make_int2(static_cast<int>(tv1[0]), static_cast<int>(tv1[1]));
+        for (int i = tid + 2 * bd; i <= rows; i += bd) prefix[i] = p.prefix_out[i];
+        for (int t = tid + 2 * bd; t < p.num_tokens; t += bd) tok[t] = p.plan_tok[t];
+        __syncthreads();
+    } else {
+        build_row_prefix(p, rows, hg_count, prefix, tok);
+        if (blockIdx.x == 0)
+            for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
+    }
+
+    auto pfx = [&](int i) { return uniform(prefix[i]); };
+    const int64_t U = pfx(rows);
+    const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
+
+    // ---- first row to visit
+    const int r_s = first_row(pfx, rows, u0);
+    // ---- empty rows of the range (kv_len <= 0): zero output (the reference would give 0/0)
+    for (int r = r_s; r < rows; ++r) {
+        const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
+        if (!(pr0 < u1 || (last_wg && pr0 == U))) break;
+        if (pr1 != pr0) continue;
+        const int t = r / hg_count, g = (r % hg_count) * wpg + wi;
+#pragma unroll
+        for (int rr = 0; rr < REP; ++rr) {
+            uint16_t* o = p.out + ((int64_t)t * H + g * REP + rr) * HD;
+            for (int dd = lane; dd < HD; dd += 64) o[dd] = 0;
+        }
+    }
+
+    // ---- pieces: the non-empty rows of [u0, u1), in order
+    auto piece_from = [&](int r, int rlim) -> Piece {
+        for (; r < rlim; ++r) {
+            const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
+            if (pr0 >= u1) break;
+            if (pr1 == pr0) continue;
+            Piece pc;
+            pc.row = r;
+            pc.t = r / hg_count;
+            pc.g = (r % hg_count) * wpg + wi;
+            const int2 tm = tok[pc.t];
+            pc.kv_len = uniform(tm.x);
+            pc.lt = static_cast<int>(max(u0, pr0) - pr0);
+            pc.le = static_cast<int>(min(u1, pr1) - pr0);
+            pc.seq = uniform(tm.y);
+            return pc;
+        }
+        Piece none;
+        none.row = -1;
+        none.t = 0;
+        none.g = wi;
+        none.kv_len = 1;
+        none.lt = 0;
+        none.le = 1;
+        none.seq = 0;
+        return none;
+    };
+
     // q slice for the REP heads of the piece's kv head, kept as raw bf16 pairs: the scores are
     // bf16 x bf16 dot products (v_dot2c_f32_bf16) against K converted fp8 -> bf16, both exact, and
     // scale*log2(e) [*k_scale] is applied to each score. Rows are processed in batches of up to
@@ -399,10 +483,12 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // reads LDS and never waits behind the K/V loads in flight.
     const float qsc = (SM == CVH_SCALE_PER_TENSOR) ? p.q_scale * p.k_scale[0] : p.q_scale;
     constexpr int QW = E / 2;                       // 32-bit words of bf16 pairs per head per lane
-    uint16_t* q_lds = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens));
+    uint16_t* q_lds = reinterpret_cast<uint16_t*>(q_lds_b);
     int rb = r_s;                        // first row of the current batch of up to qrows rows
-    auto stage_q = [&](int rlim) {       // q of rows [rb, rlim) -> LDS, this wave's head
-        for (int r = rb; r < rlim; ++r) {
+    // a planned launch has staged the first kPreQRows rows of its first batch already
+    preQ = PLANNED && r_s == plan_rs;
+    auto stage_q = [&](int r0, int rlim) {   // q of rows [r0, rlim) -> LDS, this wave's head
+        for (int r = r0; r < rlim; ++r) {
             const int t = r / hg_count, g = (r % hg_count) * wpg + wi;
             const uint16_t* src = p.q + ((int64_t)t * H + g * REP) * HD;
             uint16_t* dst = q_lds + ((r - rb) * wpg + wi) * (REP * HD);
@@ -554,7 +640,6 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         Piece pa_ = piece_from(rb, rlim);
         if (pa_.row >= 0) {
             int ta_ = pa_.lt;
-            Tile A, B, C;
             Piece pb_, pc_;
             int tb_, tc_;
             Piece lp = pa_;              // load cursor (the tile after the newest buffered one)
@@ -566,15 +651,20 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                     lt = lp.lt;
                 }
             };
-            // the first two tiles are in flight before q is staged: their latency covers it
-            load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
+            // the first two tiles are in flight before q is staged: their latency covers it (a
+            // planned launch issued them at its start when they are the plan's)
+            preA = preA && pa_.row == plan_row && ta_ == plan_lt;
+            if (!preA) load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
             advance();
             pb_ = lp;
             tb_ = lt;
-            load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
+            preB = preB && preA && pb_.row == pa_.row && tb_ == ta_ + 1;
+            if (!preB) load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
+            preA = preB = false;
             advance();
             Phys ph = lookup(lp, lt);
-            stage_q(rlim);
+            stage_q(preQ ? min(rlim, rb + kPreQRows) : rb, rlim);
+            preQ = false;
             take_q(pa_);
             reset();
             for (;;) {
@@ -617,6 +707,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             }
         }
         rb = rlim;
+        preQ = false;
     }
 }
 
@@ -675,6 +766,56 @@ __global__ __launch_bounds__(512) void paged_merge_kernel(uint16_t* __restrict__
     }
 }
 
+// Plan of a batch layout, built once and shared by every launch over the same block tables,
+// token_seq, token_kv_len and partition count (the 28 layers of a decode step): the row
+// prefix and token metadata the decode workgroups would derive, and each workgroup's first
+// piece with the physical blocks of its first two tiles. One workgroup; the same first-row
+// search and piece rules as the decode kernel.
+__global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* plan, int G, int one_block) {
+    extern __shared__ int prefix[];
+    const int hg_count = p.n_kv / p.wpg;
+    const int rows = p.num_tokens * hg_count;
+    int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows));
+    build_row_prefix(p, rows, hg_count, prefix, tok);
+    for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
+    for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) p.plan_tok[t] = tok[t];
+    const int64_t U = prefix[rows];
+    const int log2_bs = p.log2_bs;
+    auto pf = [&](int i) { return prefix[i]; };
+    for (int w = threadIdx.x; w < G; w += blockDim.x) {
+        const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
+        const int r_s = first_row(pf, rows, u0);
+        const int rlim = min(rows, r_s + p.qrows);
+        PlanRec rec = {};
+        rec.row = -1;
+        rec.r_s = r_s;
+        for (int r = r_s; r < rlim; ++r) {
+            const int64_t pr0 = prefix[r], pr1 = prefix[r + 1];
+            if (pr0 >= u1) break;
+            if (pr1 == pr0) continue;
+            const int t = r / hg_count;
+            rec.row = r;
+            rec.lt = static_cast<int>(max(u0, pr0) - pr0);
+            rec.le = static_cast<int>(min(u1, pr1) - pr0);
+            rec.kv_len = tok[t].x;
+            rec.seq = tok[t].y;
+            break;
+        }
+        if (rec.row >= 0) {
+            const int64_t* table = p.block_tables + static_cast<int64_t>(rec.seq) * p.table_width;
+            auto phys = [&](int tile, int64_t& lo, int64_t& hi) {
+                const int p0 = tile * kTileKeys;
+                lo = max(table[p0 >> log2_bs], int64_t{0});
+                hi = one_block ? lo : max(table[min(p0 + kTileKeys / 2, rec.kv_len - 1) >> log2_bs], int64_t{0});
+            };
+            phys(rec.lt, rec.a_lo, rec.a_hi);
+            rec.b_ok = rec.lt + 1 < rec.le;
+            if (rec.b_ok) phys(rec.lt + 1, rec.b_lo, rec.b_hi);
+        }
+        plan[w] = rec;
+    }
+}
+
 // ---- host side ------------------------------------------------------------------------------------
 int ilog2_pow2(int64_t v) {
     if (v <= 0 || (v & (v - 1)) != 0) return -1;
@@ -700,8 +841,9 @@ int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
 }
 
 // Workspace: prefix int32 [rows + 1] | part_acc float [G][2][WPG][REP][HD] | part_ml float2 [...]
+// | plan: token metadata int2 [T], workgroup records PlanRec [G]
 struct Workspace {
-    size_t prefix_off, acc_off, ml_off, total;
+    size_t prefix_off, acc_off, ml_off, tok_off, plan_off, total;
 };
 size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
 Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
@@ -712,11 +854,14 @@ Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
     w.prefix_off = 0;
     w.acc_off = align256(static_cast<size_t>(rows + 1) * sizeof(int));
     w.ml_off = w.acc_off + align256(static_cast<size_t>(slots) * HD * sizeof(float));
-    w.total = w.ml_off + align256(static_cast<size_t>(slots) * 2 * sizeof(float));
+    w.tok_off = w.ml_off + align256(static_cast<size_t>(slots) * 2 * sizeof(float));
+    w.plan_off = w.tok_off + align256(static_cast<size_t>(T) * sizeof(int2));
+    w.total = w.plan_off + align256(static_cast<size_t>(G) * sizeof(PlanRec));
     return w;
 }
 
-enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3 };
+// kPhasePlanned: the decode phase reads the plan kPhasePlan left in the workspace
+enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3, kPhasePlanned = 4, kPhasePlan = 8 };
 
 template <typename K>
 void launch_with_lds(K kernel, int G, int threads, size_t lds, hipStream_t s, const Params& p) {
@@ -726,21 +871,29 @@ void launch_with_lds(K kernel, int G, int threads, size_t lds, hipStream_t s, co
     kernel<<<dim3(G), threads, lds, s>>>(p);
 }
 
-template <int HD, int REP, int SM>
-void launch_decode(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
+template <int HD, int REP, int SM, bool PLANNED>
+void launch_decode_p(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
     if (one_block)
-        launch_with_lds(paged_decode_kernel<HD, REP, SM, true>, G, threads, lds, s, p);
+        launch_with_lds(paged_decode_kernel<HD, REP, SM, true, PLANNED>, G, threads, lds, s, p);
     else
-        launch_with_lds(paged_decode_kernel<HD, REP, SM, false>, G, threads, lds, s, p);
+        launch_with_lds(paged_decode_kernel<HD, REP, SM, false, PLANNED>, G, threads, lds, s, p);
+}
+template <int HD, int REP, int SM>
+void launch_decode(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block, bool planned) {
+    if (planned)
+        launch_decode_p<HD, REP, SM, true>(G, threads, lds, s, p, one_block);
+    else
+        launch_decode_p<HD, REP, SM, false>(G, threads, lds, s, p, one_block);
 }
 
 template <int HD, int SM>
-bool launch_decode_rep(int rep, int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
+bool launch_decode_rep(int rep, int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block,
+                       bool planned) {
     switch (rep) {
-        case 1: launch_decode<HD, 1, SM>(G, threads, lds, s, p, one_block); return true;
-        case 2: launch_decode<HD, 2, SM>(G, threads, lds, s, p, one_block); return true;
-        case 4: launch_decode<HD, 4, SM>(G, threads, lds, s, p, one_block); return true;
-        case 8: launch_decode<HD, 8, SM>(G, threads, lds, s, p, one_block); return true;
+        case 1: launch_decode<HD, 1, SM>(G, threads, lds, s, p, one_block, planned); return true;
+        case 2: launch_decode<HD, 2, SM>(G, threads, lds, s, p, one_block, planned); return true;
+        case 4: launch_decode<HD, 4, SM>(G, threads, lds, s, p, one_block, planned); return true;
+        case 8: launch_decode<HD, 8, SM>(G, threads, lds, s, p, one_block, planned); return true;
         default: return false;
     }
 }
@@ -753,7 +906,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0 || partitions < 0)
         return CVH_ERR_INVALID_ARG;
     if (num_tokens == 0) return CVH_OK;
-    if (!out || !q || !k_cache || !v_cache || !k_scale || !v_scale || !block_tables || !token_seq || !token_kv_len)
+    if (!block_tables || !token_seq || !token_kv_len) return CVH_ERR_INVALID_ARG;
+    if ((phase & (kPhaseDecode | kPhaseMerge)) && (!out || !q || !k_cache || !v_cache || !k_scale || !v_scale))
         return CVH_ERR_INVALID_ARG;
     if (table_width == 0) return CVH_ERR_INVALID_ARG;
     if (n_heads % n_kv_heads != 0) return CVH_ERR_UNSUPPORTED;
@@ -777,6 +931,9 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     Params p;
     p.out = static_cast<uint16_t*>(out);
     p.prefix_out = reinterpret_cast<int*>(wsb + wl.prefix_off);
+    PlanRec* plan = reinterpret_cast<PlanRec*>(wsb + wl.plan_off);
+    p.plan = plan;
+    p.plan_tok = reinterpret_cast<int2*>(wsb + wl.tok_off);
     p.part_acc = reinterpret_cast<float*>(wsb + wl.acc_off);
     p.part_ml = reinterpret_cast<float*>(wsb + wl.ml_off);
     p.q = static_cast<const uint16_t*>(q);
@@ -798,18 +955,28 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     p.q_scale = static_cast<float>(scale) * kLog2e;
 
     auto s = reinterpret_cast<hipStream_t>(stream);
+    if (phase & kPhasePlan) {
+        const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens));
+        const bool one_block = (1 << lg) >= kTileKeys;
+        if (lds > 65536)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(paged_plan_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        paged_plan_kernel<<<1, 1024, lds, s>>>(p, plan, G, one_block ? 1 : 0);
+        if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
+    }
     if (phase & kPhaseDecode) {
+        const bool planned = (phase & kPhasePlanned) != 0;
         const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens)) +
                            static_cast<size_t>(p.qrows) * wpg * rep * head_dim * 2;
         const bool one_block = (1 << lg) >= kTileKeys;
         bool ok;
         if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
             ok = head_dim == 128
-                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block)
-                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block);
+                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block, planned)
+                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block, planned);
         else
-            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block)
-                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block);
+            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block, planned)
+                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block, planned);
         if (!ok) return CVH_ERR_UNSUPPORTED;
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
@@ -875,6 +1042,21 @@ extern "C" int cvh_paged_attention_fp8_split_phase(CVH_PA_PARAMS) {
 }
 extern "C" int cvh_paged_attention_fp8_merge_phase(CVH_PA_PARAMS) {
     return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseMerge);
+}
+extern "C" int cvh_paged_attention_fp8_planned(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseBoth | cvh::kPhasePlanned);
+}
+extern "C" int cvh_paged_attention_fp8_planned_split_phase(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseDecode | cvh::kPhasePlanned);
+}
+extern "C" int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
+                                        const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads,
+                                        int head_dim, int block_size, int partitions, void* workspace,
+                                        size_t workspace_bytes, cvh_stream_t stream) {
+    return cvh::paged_attention(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, block_tables, table_width,
+                                token_seq, token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size,
+                                CVH_SCALE_PER_TOKEN_HEAD, 1.0, partitions, workspace, workspace_bytes, stream,
+                                cvh::kPhasePlan);
 }
 
 extern "C" int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,

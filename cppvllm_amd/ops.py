@@ -50,13 +50,30 @@ def paged_attention_workspace(num_tokens: int, n_heads: int, n_kv_heads: int, he
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
+def paged_attention_plan(block_tables, token_seq, token_kv_len, n_heads: int, n_kv_heads: int, head_dim: int,
+                         block_size: int, workspace: torch.Tensor, partitions: int = 0) -> None:
+    """Build the per-step plan that ``paged_attention_fp8(..., planned=True)`` reads from `workspace`
+    (once per batch layout, before the layers of a step)."""
+    T = token_seq.size(0)
+    if T == 0:
+        return
+    _require_cuda(block_tables, token_seq, token_kv_len, workspace)
+    code = _lib.lib().cvh_paged_attention_plan(
+        block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(), token_kv_len.data_ptr(), T,
+        int(n_heads), int(n_kv_heads), int(head_dim), int(block_size), int(partitions), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(token_seq))
+    check("paged_attention_plan", code)
+
+
 def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len,
-                        scale: float, *, workspace: torch.Tensor | None = None, partitions: int = 0) -> None:
+                        scale: float, *, workspace: torch.Tensor | None = None, partitions: int = 0,
+                        planned: bool = False) -> None:
     """FP8 paged attention over a ragged batch of query tokens (kernels/paged_attention.cu:459-473).
 
     out, q: bf16 [T, H, HD]; k_cache, v_cache: uint8 [NB, BS, KV, HD]; k_scale, v_scale: float32
     [NB, BS, KV] (memory order [NB][KV][BS]) or one element each (per-tensor); block_tables int64
-    [S, W]; token_seq, token_kv_len int64 [T].
+    [S, W]; token_seq, token_kv_len int64 [T]. planned=True reads the plan that
+    ``paged_attention_plan`` left in `workspace` for the same layout.
     """
     T = q.size(0)
     if T == 0:
@@ -66,8 +83,11 @@ def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables
     BS, KV = k_cache.size(1), k_cache.size(2)
     W = block_tables.size(1)
     if workspace is None:
+        if planned:
+            raise ValueError("planned=True needs the workspace the plan was built in")
         workspace = paged_attention_workspace(T, H, KV, HD, W, BS, partitions, q.device)
-    code = _lib.lib().cvh_paged_attention_fp8_ex(
+    fn = _lib.lib().cvh_paged_attention_fp8_planned if planned else _lib.lib().cvh_paged_attention_fp8_ex
+    code = fn(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
         v_scale.data_ptr(), block_tables.data_ptr(), W, token_seq.data_ptr(), token_kv_len.data_ptr(), T, H, KV,
         HD, BS, _scale_mode(k_scale), float(scale), int(partitions), workspace.data_ptr(),

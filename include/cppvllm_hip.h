@@ -106,6 +106,34 @@ int cvh_paged_attention_fp8_merge_phase(void* out, const void* q, const uint8_t*
                                         int block_size, int scale_mode, double scale, int partitions,
                                         void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 
+/* Planned launches. A decode step runs the same attention layout (block tables, token_seq,
+ * token_kv_len, partition count) once per layer; cvh_paged_attention_plan builds, once, what
+ * every decode workgroup would otherwise derive at the start of each launch (row prefix, token
+ * metadata, its first tiles' physical blocks) into the workspace, and the _planned calls read it,
+ * so each layer's first K/V loads go out one memory round trip after launch instead of three.
+ * Contract: the plan describes the arguments it was built from; rebuild it (stream-ordered before
+ * the planned calls) whenever block_tables contents, token_seq, token_kv_len, num_tokens or
+ * partitions change. Output equals cvh_paged_attention_fp8_ex bit for bit.
+ * (No reference counterpart: the reference re-derives per call; its per-step metadata is built in
+ *  model/model_architecture.cpp:137-147, where an engine would call the plan.) */
+int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
+                             const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads,
+                             int head_dim, int block_size, int partitions, void* workspace, size_t workspace_bytes,
+                             cvh_stream_t stream);
+int cvh_paged_attention_fp8_planned(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                    const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                    int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                                    int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                                    int scale_mode, double scale, int partitions, void* workspace,
+                                    size_t workspace_bytes, cvh_stream_t stream);
+int cvh_paged_attention_fp8_planned_split_phase(void* out, const void* q, const uint8_t* k_cache,
+                                                const uint8_t* v_cache, const float* k_scale, const float* v_scale,
+                                                const int64_t* block_tables, int64_t table_width,
+                                                const int64_t* token_seq, const int64_t* token_kv_len,
+                                                int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                                int block_size, int scale_mode, double scale, int partitions,
+                                                void* workspace, size_t workspace_bytes, cvh_stream_t stream);
+
 /* Workspace bytes needed by the calls above (replaces the per-call at::empty of
  * kernels/paged_attention.cu:415-421, which cannot run under graph capture). */
 size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,

@@ -248,3 +248,69 @@ def test_split_and_merge_phases_equal_combined_call():
     assert lib.cvh_paged_attention_fp8_merge_phase(*args) == 0
     torch.cuda.synchronize()
     assert np.array_equal(bits(out), base)
+
+
+def run_planned(b, partitions=0, ws=None):
+    T, H, HD = b["q"].shape
+    KV, BS, W = b["n_kv_heads"], b["block_size"], b["block_tables"].shape[1]
+    if ws is None:
+        ws = ops.paged_attention_workspace(T, H, KV, HD, W, BS, partitions, DEV)
+        ops.paged_attention_plan(b["block_tables"], b["token_seq"], b["token_kv_len"], H, KV, HD, BS, ws, partitions)
+    out = torch.empty_like(b["q"])
+    ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"], b["block_tables"],
+                            b["token_seq"], b["token_kv_len"], b["scale"], workspace=ws, partitions=partitions,
+                            planned=True)
+    torch.cuda.synchronize()
+    return bits(out)
+
+
+def _planned_case(name):
+    if name == "config1_per_tensor":
+        return workloads.config1(device="cpu", per_tensor=True), 0
+    if name == "bs16_two_block_tiles":
+        return synth(61, [40, 300, 1000, 17, 33], 16), 0
+    if name == "chunked_prefill":
+        return synth(62, [40, 300, 1000], 16, queries_per_seq=37), 0
+    if name == "empty_rows":
+        b = synth(63, [100, 50, 700, 1], 256)
+        b["token_kv_len"][1] = 0
+        return b, 0
+    if name == "partitions_7":
+        return synth(64, [3000, 100, 1400], 16), 7
+    if name == "partitions_511":
+        return synth(65, [3000, 100, 1400, 64], 64), 511
+    if name == "gqa4_hd64":
+        return synth(66, [500, 900], 32, H=16, KV=4, HD=64), 0
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("name", ["config1_per_tensor", "bs16_two_block_tiles", "chunked_prefill", "empty_rows",
+                                  "partitions_7", "partitions_511", "gqa4_hd64"])
+def test_planned_equals_unplanned_bitwise(name):
+    say(f"planned == unplanned: {name}")
+    b, parts = _planned_case(name)
+    db = dev(b)
+    assert np.array_equal(run_planned(db, parts), run_gpu(db, parts))
+
+
+def test_plan_shared_by_layers_config3(orc):
+    # one plan, two layers with different caches (the decode-step pattern); each equals the
+    # unplanned call bitwise, and layer 0 matches the oracle
+    say("config3: one plan, two layers")
+    b = workloads.config3(device=DEV)
+    T, H, HD = b["q"].shape
+    KV, BS, W = b["n_kv_heads"], b["block_size"], b["block_tables"].shape[1]
+    ws = ops.paged_attention_workspace(T, H, KV, HD, W, BS, 0, DEV)
+    ops.paged_attention_plan(b["block_tables"], b["token_seq"], b["token_kv_len"], H, KV, HD, BS, ws)
+    b2 = dict(b)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    b2["k_cache"] = torch.randint(0, 126, b["k_cache"].shape, dtype=torch.uint8, device=DEV, generator=g)
+    b2["v_cache"] = torch.randint(0, 126, b["v_cache"].shape, dtype=torch.uint8, device=DEV, generator=g)
+    got1 = run_planned(b, ws=ws)
+    got2 = run_planned(b2, ws=ws)
+    assert np.array_equal(got1, run_gpu(b))
+    assert np.array_equal(got2, run_gpu(b2))
+    assert not np.array_equal(got1, got2)
+    rows = list(range(0, T, 16))
+    cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in b.items()}
+    assert_close_bf16(got1[rows], run_oracle(orc, cpu, rows=rows))

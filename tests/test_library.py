@@ -40,6 +40,11 @@ def test_argument_validation_without_device():
     assert lib.cvh_paged_attention_fp8(*args, 4, p, p, 4, 16, 8, 128, 24, 0, 0.1, None, 0, None) == unsup
     assert lib.cvh_paged_attention_fp8(*args, 4, p, p, 4, 16, 8, 128, 8, 0, 0.1, None, 0, None) == unsup
     assert lib.cvh_paged_attention_fp8_ex(*args, 4, p, p, 4, 16, 8, 128, 16, 0, 0.1, -3, None, 0, None) == bad
+    # the plan needs only the metadata pointers and a workspace
+    assert lib.cvh_paged_attention_plan(None, 4, p, p, 4, 16, 8, 128, 16, 0, p, 1 << 30, None) == bad
+    assert lib.cvh_paged_attention_plan(p, 4, p, p, 4, 16, 8, 128, 16, 0, None, 0, None) == _lib.CVH_ERR_WORKSPACE
+    assert lib.cvh_paged_attention_fp8_planned(*args, 4, p, p, 4, 16, 8, 96, 16, 0, 0.1, 0, p, 1 << 30,
+                                               None) == unsup
     # workspace missing
     assert lib.cvh_paged_attention_fp8_ex(*args, 8, p, p, 4, 16, 8, 128, 16, 0, 0.1, 64, None, 0,
                                           None) == _lib.CVH_ERR_WORKSPACE
@@ -65,7 +70,8 @@ def test_partition_policy_and_workspace_sizes():
     assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 256
     rows, slots = 256, 256 * 2 * 16     # [G][2][WPG*REP] partial slots
     r256 = lambda v: (v + 255) // 256 * 256
-    want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4)
+    # plan: int2 token metadata [T] + 64-byte workgroup records [G]
+    want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4) + r256(256 * 8) + r256(256 * 64)
     assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == want
     # small batches: never less than two tiles per partition
     assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
