@@ -53,8 +53,26 @@ def _run(cmd: list[str]) -> None:
         sys.stderr.write(line + "\n")
 
 
+ENGINE_LIB = PKG / "libcvh_engine.so"
+ENGINE_SOURCES = ["engine_core.cpp"]
+
+
+def build_engine(verbose: bool = False) -> Path:
+    """Compile the host-only serving core (scheduler, block manager) with g++."""
+    tmp = ENGINE_LIB.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++17", "-O2", "-Wall", "-Wextra", "-fPIC", "-shared", "-o", str(tmp),
+           *[str(CSRC / s) for s in ENGINE_SOURCES]]
+    if verbose:
+        print(" ".join(cmd))
+    _run(cmd)
+    os.replace(tmp, ENGINE_LIB)
+    return ENGINE_LIB
+
+
 def build(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library. Returns its path."""
+    """Compile every HIP source for gfx950 and link the shared library (and the host serving
+    core). Returns the HIP library's path."""
+    build_engine(verbose)
     hipcc = _hipcc()
     OBJ_DIR.mkdir(exist_ok=True)
     objs = []
