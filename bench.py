@@ -74,6 +74,59 @@ def cpu_baseline(b, reps: int = 5):
                       f"median of {reps} after 1 warm-up: {med * 1e3:.1f} ms/layer"}
 
 
+def e2e_requests(seed: int = 1005, n: int = 256):
+    """Config 5's workload (bench.cpp:13-45): n prompts of U{100..1024} random token ids in
+    [0, 10000], output lengths U{100..1024}, greedy, EOS ignored. Seeded numpy draws."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, 10001, size=int(rng.integers(100, 1025))).tolist() for _ in range(n)]
+    outs = [int(x) for x in rng.integers(100, 1025, size=n)]
+    return prompts, outs
+
+
+def run_e2e(args):
+    """Config 5: end-to-end generation through the engine (continuous batching, chunked prefill,
+    HIP-graph decode) with a random-init Qwen3-0.6B; output tokens/s on one GPU."""
+    import torch
+
+    from cppvllm_amd.llm_engine import EngineConfig, LLMEngine, SamplingParams
+
+    t_init = time.perf_counter()
+    cfg = EngineConfig(max_num_batched_tokens=4096, max_num_seqs=256, max_chunk_tokens=1024, max_model_len=4096,
+                       block_size=args.e2e_block_size, seed=0, enforce_eager=args.eager)
+    eng = LLMEngine(cfg)
+    init_s = time.perf_counter() - t_init
+    eng.generate([[1, 2, 3, 4, 5, 6, 7, 8]], SamplingParams(max_tokens=16, ignore_eos=True))   # warm-up
+    prompts, outs = e2e_requests(n=args.e2e_requests)
+    before = eng.stats()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for p, n in zip(prompts, outs):
+        eng.add_request(p, SamplingParams(max_tokens=n, ignore_eos=True))
+    steps = 0
+    while not eng.is_finished():
+        eng.step()
+        steps += 1
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    got = eng.take_finished()
+    total = sum(len(v) for v in got.values())
+    assert total == sum(outs), (total, sum(outs))
+    after = eng.stats()
+    return {
+        "metric": "e2e output tok/s (config 5)", "value": round(total / dt, 2), "unit": "tok/s",
+        "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": round(dt * 1e3 / max(steps, 1), 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init Qwen3-0.6B weights N(0,0.02); seeded random prompt ids)",
+        "config": {"workload": "BASELINE config 5: 256 requests, input U(100,1024), output U(100,1024), greedy, "
+                               "ignore EOS; continuous batching, chunked prefill, HIP-graph decode",
+                   "requests": len(prompts), "output_tokens": total, "prompt_tokens": sum(len(p) for p in prompts),
+                   "seconds": round(dt, 3), "block_size": cfg.block_size, "kv_blocks": eng.num_blocks,
+                   "preemptions": after.preemptions - before.preemptions, "init_s": round(init_s, 1),
+                   "launch": "eager" if args.eager else "hip_graph"},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -88,6 +141,9 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=(3, 4),
                     help="3: 256 seqs, ctx U(100,1024)+U(0,1024) (headline); 4: 64 seqs, ctx log-U(4k,32k)")
     ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
+    ap.add_argument("--e2e", action="store_true", help="config 5: end-to-end generation tok/s through the engine")
+    ap.add_argument("--e2e-requests", type=int, default=256)
+    ap.add_argument("--e2e-block-size", type=int, default=256)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain 1 GiB device-to-device copies (rocprofv3 FETCH/WRITE_SIZE scale)")
     args = ap.parse_args()
@@ -103,6 +159,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.e2e:
+        print(json.dumps(run_e2e(args)), flush=True)
+        return
     if args.calibrate_copy:
         a = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
         c = torch.empty_like(a)

@@ -52,6 +52,10 @@ SIGNATURES = {
     "cvh_build_token_metadata": (i32, [vp, i64, vp, i64, vp, i64, i32, vp, vp, vp, vp]),
     "cvh_rope_tables_host": (i32, [vp, vp, i64, i32, f64]),
     "cvh_fp8_e4m3_quantize": (i32, [vp, vp, i64, f32, vp]),
+    "cvh_swiglu": (i32, [vp, vp, i64, i32, i32, vp]),
+    "cvh_sample_tokens": (i32, [vp, vp, i32, vp, vp, i64, i32, C.c_uint64, C.c_uint64, vp]),
+    "cvh_feed_tokens": (i32, [vp, vp, vp, i64, vp]),
+    "cvh_embedding": (i32, [vp, vp, vp, i64, i32, i64, vp]),
     "cvh_version": (C.c_char_p, []),
 }
 

@@ -8,6 +8,7 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -32,6 +33,7 @@ SOURCES = {
     "fused_ops.hip": ["-ffp-contract=off"],
     "paged_attention.hip": [],
     "batch_metadata.hip": ["-ffp-contract=off"],
+    "model_ops.hip": ["-ffp-contract=off"],
 }
 
 
@@ -75,14 +77,16 @@ def build(verbose: bool = False) -> Path:
     build_engine(verbose)
     hipcc = _hipcc()
     OBJ_DIR.mkdir(exist_ok=True)
-    objs = []
+    objs, cmds = [], []
     for src, extra in SOURCES.items():
         obj = OBJ_DIR / (Path(src).stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd))
-        _run(cmd)
+        cmds.append([hipcc, *HIPCC_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
+        if verbose:
+            print(" ".join(cmds[-1]))
+    # one hipcc per source, in parallel (each is single-threaded)
+    with ThreadPoolExecutor(max_workers=min(len(cmds), os.cpu_count() or 1)) as pool:
+        list(pool.map(_run, cmds))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *objs]
     if verbose:

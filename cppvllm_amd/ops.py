@@ -128,9 +128,52 @@ def _qk_norm_rope_kv_write_fp8(q_out, qkv, q_norm, k_norm, cos, sin, positions, 
     check("qk_norm_rope_kv_write_fp8", code)
 
 
+def _swiglu(out, gate_up) -> None:
+    """out [T, I] = silu(gate) * up over gate_up [T, 2I] (kernels/fused_ops.cu:261-283)."""
+    if out.numel() == 0:
+        return
+    _require_cuda(out, gate_up)
+    if gate_up.dtype != out.dtype or gate_up.size(-1) != 2 * out.size(-1):
+        raise ValueError("swiglu: gate_up must be [T, 2I] of out's dtype")
+    check("swiglu", _lib.lib().cvh_swiglu(out.data_ptr(), gate_up.data_ptr(), out.size(0), out.size(1),
+                                          _DT[out.dtype], _stream(out)))
+
+
+def _sample_tokens(out, logits, rows, temps, seed: int, offset: int) -> None:
+    """out int64 [R] = sampled token of logits row rows[r] (kernels/fused_ops.cu:367-378); rows or
+    temps may be None (all rows / greedy)."""
+    R = out.numel() if rows is None else rows.numel()
+    if R == 0:
+        return
+    _require_cuda(out, logits, rows, temps)
+    ldt = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}[logits.dtype]
+    check("sample_tokens", _lib.lib().cvh_sample_tokens(out.data_ptr(), logits.data_ptr(), ldt, _ptr(rows),
+                                                        _ptr(temps), R, logits.size(1), int(seed) & (2**64 - 1),
+                                                        int(offset) & (2**64 - 1), _stream(logits)))
+
+
+def _feed_tokens(tokens, src, prev) -> None:
+    """tokens[i] = prev[src[i]] where src[i] >= 0 (kernels/fused_ops.cu:388-397)."""
+    if tokens.numel() == 0:
+        return
+    _require_cuda(tokens, src, prev)
+    check("feed_tokens", _lib.lib().cvh_feed_tokens(tokens.data_ptr(), src.data_ptr(), prev.data_ptr(),
+                                                    tokens.numel(), _stream(tokens)))
+
+
 # The reference's `namespace fused` (kernels/fused_ops.h:5).
 fused = types.SimpleNamespace(rms_norm=_rms_norm, add_rms_norm=_add_rms_norm,
-                              qk_norm_rope_kv_write_fp8=_qk_norm_rope_kv_write_fp8)
+                              qk_norm_rope_kv_write_fp8=_qk_norm_rope_kv_write_fp8, swiglu=_swiglu,
+                              sample_tokens=_sample_tokens, feed_tokens=_feed_tokens)
+
+
+def embedding(out, table, ids) -> None:
+    """out [T, D] = table[ids] for 16-bit tables (model/model_architecture.cpp:149)."""
+    if ids.numel() == 0:
+        return
+    _require_cuda(out, table, ids)
+    check("embedding", _lib.lib().cvh_embedding(out.data_ptr(), table.data_ptr(), ids.data_ptr(), ids.numel(),
+                                                table.size(1), table.size(0), _stream(out)))
 
 
 def build_token_metadata(cu_seqlens, positions, block_tables, block_size: int):

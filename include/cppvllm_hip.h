@@ -201,6 +201,38 @@ int cvh_rope_tables_host(float* cos_t, float* sin_t, int64_t max_position, int h
  * (reference: __nv_cvt_float_to_fp8(x, __NV_SATFINITE, __NV_E4M3), kernels/fused_ops.cu:42-44). */
 int cvh_fp8_e4m3_quantize(uint8_t* dst, const float* src, int64_t n, float inv_scale, cvh_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Model ops around the attention path (used by the serving loop; not part of the decode kernel).
+ * ------------------------------------------------------------------------------------------- */
+
+/* SwiGLU: gate_up [num_rows][2*intermediate] (gate half first), out [num_rows][intermediate]:
+ *   silu = round(g / (1 + exp(-g))) (exp evaluated in double), out = round(silu * u).
+ * Replaces: void fused::swiglu(at::Tensor& out, const at::Tensor& gate_up)
+ *           (kernels/fused_ops.h:17, kernels/fused_ops.cu:209-220,261-283). dtype: CVH_DTYPE_*. */
+int cvh_swiglu(void* out, const void* gate_up, int64_t num_rows, int intermediate, int dtype, cvh_stream_t stream);
+
+/* Token sampler: out[r] = arg-max over the vocab of row rows[r] of logits (rows == NULL: row r).
+ * temps[r] <= 0 (or temps == NULL): greedy, lowest index wins ties. temps[r] > 0: Gumbel-max,
+ * score = x/temp - log(-log(u)), u from Philox-4x32-10 keyed by seed with counter
+ * (index/4, r, offset lo, offset hi). logits_dtype: CVH_DTYPE_F32 or CVH_DTYPE_BF16 (same values
+ * as the reference's float copy of bf16 logits).
+ * Replaces: void fused::sample_tokens(at::Tensor& out, const at::Tensor& logits, const at::Tensor& rows,
+ *           const at::Tensor& temps, uint64_t seed, uint64_t offset)
+ *           (kernels/fused_ops.h:19-20, kernels/fused_ops.cu:285-378). */
+int cvh_sample_tokens(int64_t* out, const void* logits, int logits_dtype, const int64_t* rows, const float* temps,
+                      int64_t num_rows, int vocab, uint64_t seed, uint64_t offset, cvh_stream_t stream);
+
+/* Token feedback: tokens[i] = prev[src[i]] where src[i] >= 0.
+ * Replaces: void fused::feed_tokens(at::Tensor& tokens, const at::Tensor& src, const at::Tensor& prev)
+ *           (kernels/fused_ops.h:22, kernels/fused_ops.cu:379-397). */
+int cvh_feed_tokens(int64_t* tokens, const int64_t* src, const int64_t* prev, int64_t n, cvh_stream_t stream);
+
+/* Embedding gather of 16-bit rows: out[t] = table[ids[t]] ([num_tokens][dim], dim % 8 == 0);
+ * ids outside [0, vocab) give a zero row. Replaces embed_.index_select(0, tokens)
+ * (model/model_architecture.cpp:149). */
+int cvh_embedding(void* out, const void* table, const int64_t* ids, int64_t num_tokens, int dim, int64_t vocab,
+                  cvh_stream_t stream);
+
 /* Library version string (static storage). */
 const char* cvh_version(void);
 

@@ -24,6 +24,11 @@ How each function is pinned (independently of the code it checks; tests/test_ora
                     permutation invariance of physical block ids.
   * token_metadata — numpy searchsorted(right=True) + gather closed form.
   * rope tables   — numpy float64 cos/sin of pos * theta^(-2i/hd).
+  * swiglu        — numpy float64 silu then the two roundings via torch casts; g = 0 => 0,
+                    large |g| limits (silu(g) -> g, -> -0).
+  * philox4x32_10 — the Random123 known-answer vectors for philox4x32_10.
+  * sample_tokens — numpy argmax (first maximum) for greedy rows; Gumbel rows: the u stream's
+                    closed form from the KAT-pinned Philox and a numpy float64 score + argmax.
 There are no golden vectors in the reference (it has no tests); no function is left unpinned.
 """
 from __future__ import annotations
@@ -65,6 +70,9 @@ def lib() -> C.CDLL:
             "orc_qk_norm_rope_kv_write_fp8": (None, [vp] * 14 + [i64, i32, i32, i32, i32, i32, f64]),
             "orc_paged_attention_fp8": (None, [vp] * 7 + [i64, vp, vp, i64, i32, i32, i32, i32, i32, f64]),
             "orc_token_metadata": (None, [vp, i64, vp, i64, vp, i64, i32, vp, vp, vp]),
+            "orc_swiglu": (None, [vp, vp, i64, i32, i32]),
+            "orc_philox4x32_10": (None, [vp, C.c_uint32, C.c_uint32]),
+            "orc_sample_tokens": (None, [vp, vp, i32, vp, vp, i64, i32, C.c_uint64, C.c_uint64]),
             "orc_max_threads": (i32, []),
             "orc_set_threads": (None, [i32]),
         }
@@ -170,6 +178,35 @@ def token_metadata(cu_seqlens, positions, block_tables, block_size):
     lib().orc_token_metadata(_p(cu_seqlens), S, _p(positions), T, _p(block_tables), block_tables.shape[1],
                              block_size, _p(seq), _p(slot), _p(kvl))
     return seq, slot, kvl
+
+
+# ---- model ops around the path ------------------------------------------------------------------------
+def swiglu(gate_up: np.ndarray, dtype: int = BF16) -> np.ndarray:
+    """gate_up [N, 2I] (bf16/f16 bit patterns as uint16, or float32) -> out [N, I]."""
+    gu = np.ascontiguousarray(gate_up)
+    N, I2 = gu.shape
+    out = np.empty((N, I2 // 2), dtype=gu.dtype)
+    lib().orc_swiglu(_p(out), _p(gu), N, I2 // 2, dtype)
+    return out
+
+
+def philox4x32_10(counter, key) -> np.ndarray:
+    c = np.array(counter, dtype=np.uint32)
+    lib().orc_philox4x32_10(_p(c), int(key[0]), int(key[1]))
+    return c
+
+
+def sample_tokens(logits: np.ndarray, rows=None, temps=None, seed: int = 0, offset: int = 0) -> np.ndarray:
+    """logits float32 or bf16 bit patterns (uint16) [*, V]; rows int64 [R] (None: all rows);
+    temps float32 [R] (None: greedy)."""
+    lg = np.ascontiguousarray(logits)
+    dt = F32 if lg.dtype == np.float32 else BF16
+    R = lg.shape[0] if rows is None else len(rows)
+    rows = None if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
+    temps = None if temps is None else np.ascontiguousarray(temps, dtype=np.float32)
+    out = np.empty(R, dtype=np.int64)
+    lib().orc_sample_tokens(_p(out), _p(lg), dt, _p(rows), _p(temps), R, lg.shape[1], seed, offset)
+    return out
 
 
 if os.environ.get("CVH_ORACLE_REBUILD"):

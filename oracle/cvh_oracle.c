@@ -346,6 +346,65 @@ void orc_token_metadata(const int64_t* cu, int64_t S, const int64_t* positions, 
     }
 }
 
+/* ---- SwiGLU: restates kernels/fused_ops.cu:210-219 (silu rounded to the row dtype, then the
+ *      product rounded), with g/(1+exp(-g)) evaluated in double (the build's documented order). */
+void orc_swiglu(void* out, const void* gu, int64_t N, int I, int dt) {
+    for (int64_t r = 0; r < N; ++r)
+        for (int i = 0; i < I; ++i) {
+            float g = ld(gu, r * 2 * I + i, dt), u = ld(gu, r * 2 * I + I + i, dt);
+            float silu = rnd((float)((double)g / (1.0 + exp(-(double)g))), dt);
+            st(out, r * I + i, dt, silu * u);
+        }
+}
+
+/* ---- Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+ *      SC'11): 10 rounds of the 4x32 bijection with multipliers 0xD2511F53, 0xCD9E8D57 and the key
+ *      schedule k += (0x9E3779B9, 0xBB67AE85). Used by the sampler of kernels/fused_ops.cu:287-299. */
+void orc_philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+    for (int i = 0; i < 10; ++i) {
+        uint64_t p0 = (uint64_t)0xD2511F53u * c[0], p1 = (uint64_t)0xCD9E8D57u * c[2];
+        uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0, n1 = (uint32_t)p1;
+        uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1, n3 = (uint32_t)p0;
+        c[0] = n0; c[1] = n1; c[2] = n2; c[3] = n3;
+        k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+    }
+}
+
+/* ---- token sampler: restates kernels/fused_ops.cu:309-365 as a plain scan in index order:
+ *      greedy (temp <= 0) = arg-max, lowest index on ties; otherwise Gumbel-max with
+ *      u = ((r >> 8) + 0.5) / 2^24 from Philox counter (j/4, row, offset) and the score
+ *      x/temp - log(max(-log u, 1e-10)) evaluated in double, rounded to float. logits are f32
+ *      (dt == ORC_F32) or bf16 bit patterns. */
+void orc_sample_tokens(int64_t* out, const void* logits, int dt, const int64_t* rows, const float* temps, int64_t R,
+                       int V, uint64_t seed, uint64_t offset) {
+    for (int64_t r = 0; r < R; ++r) {
+        int64_t src = rows ? rows[r] : r;
+        float temp = temps ? temps[r] : 0.f;
+        int greedy = !(temp > 0.f);
+        float inv_t = 1.0f / fmaxf(temp, 1e-5f);
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        uint32_t c[4] = {0, 0, 0, 0};
+        for (int j = 0; j < V; ++j) {
+            float x = ld(logits, src * (int64_t)V + j, dt == ORC_F32 ? ORC_F32 : ORC_BF16), s = x;
+            if (!greedy) {
+                if ((j & 3) == 0) {
+                    c[0] = (uint32_t)(j >> 2); c[1] = (uint32_t)r;
+                    c[2] = (uint32_t)offset; c[3] = (uint32_t)(offset >> 32);
+                    orc_philox4x32_10(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+                }
+                float u = ((float)(c[j & 3] >> 8) + 0.5f) * (1.0f / 16777216.0f);
+                double e = fmax(-log((double)u), 1e-10);
+                s = (float)((double)x * inv_t - log(e));
+            }
+            /* kernels/fused_ops.cu:303: larger, or equal with a lower index (so an all -inf row
+             * gives index 0; NaN never wins) */
+            if (s > bv || (s == bv && j < bi)) { bv = s; bi = j; }
+        }
+        out[r] = bi;
+    }
+}
+
 int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -1,0 +1,82 @@
+"""GPU parity of the model ops around the attention path (SwiGLU, sampler, token feedback,
+embedding) against the CPU oracle, through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from cppvllm_amd import ops
+from tests._util import np_, say
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("T,I,dtype", [(256, 3072, torch.bfloat16), (7, 100, torch.bfloat16),
+                                       (33, 3072, torch.float16), (9, 64, torch.float32), (1, 8, torch.bfloat16)])
+def test_swiglu_bitexact(orc, T, I, dtype):
+    say(f"swiglu T={T} I={I} {dtype}")
+    g = torch.Generator().manual_seed(T * 7 + I)
+    gu = (torch.randn((T, 2 * I), generator=g) * 3).to(dtype)
+    gu[0, :4] = torch.tensor([0.0, 40.0, -40.0, 1e-3]).to(dtype)
+    out = torch.empty((T, I), dtype=dtype, device=DEV)
+    ops.fused.swiglu(out, gu.to(DEV))
+    torch.cuda.synchronize()
+    dt = {torch.bfloat16: orc.BF16, torch.float16: orc.F16, torch.float32: orc.F32}[dtype]
+    src = np_(gu) if dtype != torch.float16 else gu.view(torch.int16).numpy().view(np.uint16)
+    want = orc.swiglu(src, dtype=dt)
+    got = np_(out) if dtype != torch.float16 else out.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("ldtype", [torch.float32, torch.bfloat16])
+def test_greedy_sampler_full_vocab(orc, ldtype):
+    say(f"greedy sampler R=256 V=151936 {ldtype}")
+    g = torch.Generator().manual_seed(11)
+    R, V = 256, 151936
+    lg = torch.randn((R, V), generator=g).to(ldtype)
+    lg[3, [17, 90000, 151935]] = 40.0            # ties -> lowest index
+    lg[4, -1] = 60.0                              # max in the last element
+    lg[5, 0] = 60.0
+    lg[6, :] = float("-inf")
+    lg[7, 5] = float("nan")
+    out = torch.empty(R, dtype=torch.int64, device=DEV)
+    ops.fused.sample_tokens(out, lg.to(DEV), None, None, 0, 0)
+    torch.cuda.synchronize()
+    want = orc.sample_tokens(np_(lg))
+    got = out.cpu().numpy()
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"rows {bad[:8]}: got {got[bad[:8]]} want {want[bad[:8]]}"
+    assert want[3] == 17 and want[4] == V - 1 and want[5] == 0 and want[6] == 0
+
+
+def test_sampler_rows_and_temperatures(orc):
+    say("gumbel sampler rows/temps R=8 V=151936 and V=1003")
+    g = torch.Generator().manual_seed(12)
+    for V in (151936, 1003):
+        lg = torch.randn((10, V), generator=g)
+        rows = torch.tensor([9, 0, 3, 3, 5, 1, 2, 8], dtype=torch.int64)
+        temps = torch.tensor([0.6, 1.0, 0.0, 0.6, 2.0, -1.0, 1e-6, 0.3], dtype=torch.float32)
+        out = torch.empty(8, dtype=torch.int64, device=DEV)
+        seed, off = 0xDEADBEEF12345678, 3
+        ops.fused.sample_tokens(out, lg.to(DEV), rows.to(DEV), temps.to(DEV), seed, off)
+        torch.cuda.synchronize()
+        want = orc.sample_tokens(lg.numpy(), rows=rows.numpy(), temps=temps.numpy(), seed=seed, offset=off)
+        got = out.cpu().numpy()
+        assert np.array_equal(got, want), f"V={V}: got {got} want {want}"
+
+
+def test_feed_tokens_and_embedding():
+    say("feed_tokens / embedding")
+    prev = torch.tensor([100, 101, 102, 103], dtype=torch.int64, device=DEV)
+    tokens = torch.tensor([5, 6, 7, 8, 9], dtype=torch.int64, device=DEV)
+    src = torch.tensor([-1, 3, -1, 0, 0], dtype=torch.int64, device=DEV)
+    ops.fused.feed_tokens(tokens, src, prev)
+    assert tokens.cpu().tolist() == [5, 103, 7, 100, 100]
+    g = torch.Generator().manual_seed(13)
+    table = torch.randn((1000, 1024), generator=g).to(torch.bfloat16).to(DEV)
+    ids = torch.tensor([0, 999, 17, 17, -1, 1000], dtype=torch.int64, device=DEV)
+    out = torch.empty((6, 1024), dtype=torch.bfloat16, device=DEV)
+    ops.embedding(out, table, ids)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:4], table[ids[:4]])
+    assert torch.count_nonzero(out[4:]) == 0
