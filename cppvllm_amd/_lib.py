@@ -38,6 +38,8 @@ SIGNATURES = {
                                                   i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_merge_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32,
                                                   i32, f64, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
+                                              f64, vp]),
     "cvh_paged_attention_plan": (i32, [vp, i64, vp, vp, i64, i32, i32, i32, i32, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
                                               f64, i32, vp, sz, vp]),

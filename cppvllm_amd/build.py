@@ -32,6 +32,7 @@ HIPCC_FLAGS = [
 SOURCES = {
     "fused_ops.hip": ["-ffp-contract=off"],
     "paged_attention.hip": [],
+    "paged_prefill.hip": [],
     "batch_metadata.hip": ["-ffp-contract=off"],
     "model_ops.hip": ["-ffp-contract=off"],
 }

@@ -1,0 +1,373 @@
+// FP8-e4m3 paged attention for multi-token query rows (chunked prefill / prompt continuation)
+// on gfx950 matrix cores.
+//
+// Reference semantics: kernels/paged_attention.cu:89-359 with T > S — every query token t attends
+// causally to keys [0, token_kv_len[t]) of sequence token_seq[t] through its block table, GQA
+// query heads share the kv head, K/V dequantised with per-(token, kv head) (or per-tensor)
+// scales, softmax in fp32. The decode kernel walks one query token per row; here 16 consecutive
+// query tokens of a sequence share every K/V tile, so the score and PV products are real dense
+// contractions and run on MFMA (v_mfma_f32_16x16x32_bf16):
+//
+//   S^T[key][row] = K . Q^T   A = K   (16 keys x 32 d, e4m3 -> bf16 exact),  B = Q^T (bf16)
+//   O^T[d][row]  += V^T . P^T A = V^T (16 d x 32 keys, bf16 via LDS),        B = P^T (bf16, v scale folded)
+//
+// Both products put one query row per lane column (lane % 16), so the row's softmax state, its
+// causal mask and its output accumulators live in the same lanes with no cross-lane shuffles
+// except the 4-way max/sum over lane groups. The contraction index order inside an MFMA is
+// free as long as A and B agree: lane group g = lane / 16 supplies d in
+// {c*64 + g*16 + h*8 + 0..7} for step s = 2c + h (so each lane reads 16 contiguous K bytes per
+// chunk), and keys {g*4 + 0..3, 16 + g*4 + 0..3} for the PV step (the keys its S^T output holds).
+//
+// Work: a wave = (16 consecutive query tokens, one kv head); a workgroup = WPG waves on WPG kv
+// heads of the same tokens, so the whole 1 KB slot row of a key is read by one workgroup. Tokens
+// of different sequences inside one 16-token tile are processed as separate runs (rows outside
+// the run are masked), so any ragged batch is valid input; tiles rarely straddle sequences.
+// V tiles are transposed through a per-wave LDS region (32 keys x 128 d bf16): each lane loads
+// a 4 key x 4 d byte block with 4 dword loads, transposes it with v_perm_b32, converts to bf16 and
+// stores 4 keys of one d with ds_write_b64.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "cvh_device.h"
+
+namespace cvh {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_p __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kHD = 128;
+constexpr int kQTok = 16;          // query tokens per wave
+constexpr int kTile = 32;          // keys per tile
+constexpr int kVtStride = 40;      // bf16 per LDS row of V^T (32 keys + 8 pad): 80 bytes
+constexpr float kLog2eP = 1.4426950408889634f;
+constexpr float kNegHuge = -1e30f;
+
+template <bool HI> __device__ __forceinline__ uint32_t pk_bf16(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+
+// 8 e4m3 codes (two dwords) -> 8 bf16 (exact for finite codes)
+__device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint32_t a, uint32_t b) {
+    const uint32_t r[4] = {pk_bf16<false>(a), pk_bf16<true>(a), pk_bf16<false>(b), pk_bf16<true>(b)};
+    return __builtin_bit_cast(bf16x8_t, r);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
+
+__device__ __forceinline__ float max_groups(float v) {   // max over the 4 lane groups (lanes l, l^16, l^32, l^48)
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float sum_groups(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+template <int REP, int SCALE_MODE, int WPG>
+__global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
+        uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
+        const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
+        const int64_t* __restrict__ tables, int64_t W, const int64_t* __restrict__ token_seq,
+        const int64_t* __restrict__ token_kv_len, int T, int H, int KV, int lg_bs, float scale_log2) {
+    __shared__ __align__(16) uint16_t vt_all[WPG][kHD * kVtStride];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint16_t* vt = vt_all[w];
+    const int kvh = blockIdx.y * WPG + w;
+    const int t0 = blockIdx.x * kQTok;
+    const int g = lane >> 4, i16 = lane & 15;
+    const int BS = 1 << lg_bs, bs_mask = BS - 1;
+    const int64_t row_bytes = static_cast<int64_t>(KV) * kHD;      // one slot row, all kv heads
+
+    // this lane's query row (token t0 + i16; heads kvh*REP + rb)
+    const int tq = t0 + i16;
+    int64_t seq = -1, kvl = 0;
+    if (tq < T) {
+        seq = token_seq[tq];
+        kvl = token_kv_len[tq];
+        if (seq < 0 || kvl < 0) kvl = 0;
+        if (kvl > (W << lg_bs)) kvl = W << lg_bs;        // contexts end at the table's last block
+    }
+
+    // Q as the B operand of S^T: step s = 2c + h covers d = c*64 + g*16 + h*8 + 0..7
+    bf16x8_t qop[REP][4];
+#pragma unroll
+    for (int rb = 0; rb < REP; ++rb) {
+        const uint16_t* qr = q + (static_cast<int64_t>(tq < T ? tq : 0) * H + kvh * REP + rb) * kHD;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (tq < T) v = *reinterpret_cast<const uint4*>(qr + c * 64 + g * 16 + h * 8);
+                qop[rb][2 * c + h] = __builtin_bit_cast(bf16x8_t, v);
+            }
+    }
+
+    f32x4_t o[REP][8];
+    float m[REP], lsum[REP];
+#pragma unroll
+    for (int rb = 0; rb < REP; ++rb) {
+        m[rb] = kNegHuge;
+        lsum[rb] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[rb][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const float ks_tensor = SCALE_MODE == CVH_SCALE_PER_TENSOR ? ksc[0] : 0.f;
+    const float vs_tensor = SCALE_MODE == CVH_SCALE_PER_TENSOR ? vsc[0] : 0.f;
+
+    // runs of equal sequence among the 16 tokens (lanes 0..15 carry the rows)
+    uint64_t todo = __builtin_amdgcn_ballot_w64(lane < kQTok && kvl > 0);
+    while (todo) {
+        const int leader = __builtin_ctzll(todo);
+        const int64_t rseq =
+                static_cast<int64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(seq), leader))) |
+                (static_cast<int64_t>(__builtin_amdgcn_readlane(static_cast<int>(seq >> 32), leader)) << 32);
+        const bool in_run = seq == rseq && kvl > 0;
+        todo &= ~__builtin_amdgcn_ballot_w64(lane < kQTok && in_run);
+        int kmax_l = in_run ? static_cast<int>(kvl) : 0;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) kmax_l = max(kmax_l, __shfl_xor(kmax_l, d, 64));
+        const int kmax = __builtin_amdgcn_readfirstlane(kmax_l);
+        const int64_t* trow = tables + rseq * W;
+        const int row_kvl = in_run ? static_cast<int>(kvl) : 0;
+
+        for (int kb0 = 0; kb0 < kmax; kb0 += kTile) {
+            // physical blocks of the tile's keys (one block when BS >= 32; two when BS == 16)
+            // (a negative entry inside a context is invalid input: its keys read as zeros)
+            const int64_t blk0 = trow[kb0 >> lg_bs];
+            const int64_t blk1 = (BS < kTile && kb0 + 16 < kmax) ? trow[(kb0 + 16) >> lg_bs] : blk0;
+            auto blk_of = [&](int key) -> int64_t { return (BS < kTile && key >= 16) ? blk1 : blk0; };
+            auto live = [&](int key) -> bool { return kb0 + key < kmax && blk_of(key) >= 0; };
+            auto slot_of = [&](int key) -> int64_t {       // key offset inside the tile
+                return (blk_of(key) << lg_bs) + ((kb0 + key) & bs_mask);
+            };
+
+            // ---- K (A operand, rows = keys kb*16 + i16): 16 contiguous bytes per chunk c
+            bf16x8_t kop[2][4];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int key = kb * 16 + i16;
+                uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
+                if (live(key)) {
+                    const uint8_t* kr = kc + slot_of(key) * row_bytes + kvh * kHD + g * 16;
+                    c0 = *reinterpret_cast<const uint4*>(kr);
+                    c1 = *reinterpret_cast<const uint4*>(kr + 64);
+                }
+                kop[kb][0] = fp8x8_to_bf16(c0.x, c0.y);
+                kop[kb][1] = fp8x8_to_bf16(c0.z, c0.w);
+                kop[kb][2] = fp8x8_to_bf16(c1.x, c1.y);
+                kop[kb][3] = fp8x8_to_bf16(c1.z, c1.w);
+            }
+            // ---- V: 4 keys x 4 d bytes per lane per iteration, transposed into LDS as bf16
+            uint32_t vw[4][4];
+            {
+                const int c = lane & 31, kg = lane >> 5;
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int key = it * 8 + kg * 4 + e;
+                        vw[it][e] = 0u;
+                        if (live(key))
+                            vw[it][e] = *reinterpret_cast<const uint32_t*>(vc + slot_of(key) * row_bytes + kvh * kHD +
+                                                                           c * 4);
+                    }
+                }
+            }
+            // ---- scales of the 4 keys g*4 + r of each 16-key block (S^T output rows)
+            float ks4[2][4], vs4[2][4];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int key = kb * 16 + g * 4;
+                if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
+                    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+                    if (live(key)) {
+                        const int64_t si = ((blk_of(key) * KV + kvh) << lg_bs) + ((kb0 + key) & bs_mask);
+                        a = *reinterpret_cast<const float4*>(ksc + si);
+                        b = *reinterpret_cast<const float4*>(vsc + si);
+                    }
+                    ks4[kb][0] = a.x; ks4[kb][1] = a.y; ks4[kb][2] = a.z; ks4[kb][3] = a.w;
+                    vs4[kb][0] = b.x; vs4[kb][1] = b.y; vs4[kb][2] = b.z; vs4[kb][3] = b.w;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        ks4[kb][r] = ks_tensor;
+                        vs4[kb][r] = vs_tensor;
+                    }
+                }
+            }
+
+            // ---- S^T = K . Q^T
+            f32x4_t s[2][REP];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int rb = 0; rb < REP; ++rb) {
+                    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int st = 0; st < 4; ++st)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kb][st], qop[rb][st], acc, 0, 0, 0);
+                    s[kb][rb] = acc;
+                }
+
+            // ---- V^T into LDS (previous tile's reads were issued before these writes; LDS
+            //      operations of a wave complete in order)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            {
+                const int c = lane & 31, kg = lane >> 5;
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const uint32_t w0 = vw[it][0], w1 = vw[it][1], w2 = vw[it][2], w3 = vw[it][3];
+                    const uint32_t a = __builtin_amdgcn_perm(w1, w0, 0x05010400u);   // w0b0 w1b0 w0b1 w1b1
+                    const uint32_t b = __builtin_amdgcn_perm(w1, w0, 0x07030602u);   // w0b2 w1b2 w0b3 w1b3
+                    const uint32_t cc = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+                    const uint32_t dd = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+                    const uint32_t tr[4] = {__builtin_amdgcn_perm(cc, a, 0x05040100u),
+                                            __builtin_amdgcn_perm(cc, a, 0x07060302u),
+                                            __builtin_amdgcn_perm(dd, b, 0x05040100u),
+                                            __builtin_amdgcn_perm(dd, b, 0x07060302u)};
+                    const int key = it * 8 + kg * 4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint2 v2 = make_uint2(pk_bf16<false>(tr[e]), pk_bf16<true>(tr[e]));
+                        *reinterpret_cast<uint2*>(vt + (c * 4 + e) * kVtStride + key) = v2;
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+            // ---- scores, mask, online softmax (one query row per lane column)
+#pragma unroll
+            for (int rb = 0; rb < REP; ++rb) {
+                float mt = kNegHuge;
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = kb0 + kb * 16 + g * 4 + r;
+                        float sv = s[kb][rb][r] * (ks4[kb][r] * scale_log2);
+                        sv = key < row_kvl ? sv : -INFINITY;
+                        s[kb][rb][r] = sv;
+                        mt = fmaxf(mt, sv);
+                    }
+                mt = max_groups(mt);
+                const float mn = fmaxf(m[rb], mt);
+                const float alpha = __builtin_amdgcn_exp2f(m[rb] - mn);
+                m[rb] = mn;
+                float ps = 0.f;
+                uint32_t pp[4];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 4; r += 2) {
+                        const float p0 = __builtin_amdgcn_exp2f(s[kb][rb][r] - mn);
+                        const float p1 = __builtin_amdgcn_exp2f(s[kb][rb][r + 1] - mn);
+                        ps += p0 + p1;
+                        pp[kb * 2 + r / 2] = pack_bf16x2(p0 * vs4[kb][r], p1 * vs4[kb][r + 1]);
+                    }
+                lsum[rb] = lsum[rb] * alpha + ps;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
+                const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pp);
+                // ---- O^T += V^T . P^T over the 8 d blocks
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint16_t* vr = vt + (j * 16 + i16) * kVtStride + g * 4;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+                    const uint32_t va[4] = {lo.x, lo.y, hi.x, hi.y};
+                    o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pop,
+                                                                       o[rb][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    if (tq >= T) return;
+#pragma unroll
+    for (int rb = 0; rb < REP; ++rb) {
+        const float l = sum_groups(lsum[rb]);
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        uint16_t* orow = out + (static_cast<int64_t>(tq) * H + kvh * REP + rb) * kHD;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint2 v = make_uint2(pack_bf16x2(o[rb][j][0] * inv, o[rb][j][1] * inv),
+                                       pack_bf16x2(o[rb][j][2] * inv, o[rb][j][3] * inv));
+            *reinterpret_cast<uint2*>(orow + j * 16 + g * 4) = v;
+        }
+    }
+}
+
+int ilog2_exact(int v) {
+    if (v <= 0 || (v & (v - 1)) != 0) return -1;
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+}
+
+template <int REP, int SM>
+int launch_rep(uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_t* vc, const float* ks,
+               const float* vs, const int64_t* tables, int64_t W, const int64_t* tseq, const int64_t* tkvl, int T,
+               int H, int KV, int lg, float sl2, hipStream_t s) {
+    const unsigned gx = static_cast<unsigned>((T + kQTok - 1) / kQTok);
+#define CVH_PREFILL(WPG)                                                                                      \
+    paged_prefill_kernel<REP, SM, WPG><<<dim3(gx, KV / (WPG)), 64 * (WPG), 0, s>>>(out, q, kc, vc, ks, vs, tables, \
+                                                                                   W, tseq, tkvl, T, H, KV, lg, sl2)
+    if (KV % 8 == 0) CVH_PREFILL(8);
+    else if (KV % 4 == 0) CVH_PREFILL(4);
+    else if (KV % 2 == 0) CVH_PREFILL(2);
+    else CVH_PREFILL(1);
+#undef CVH_PREFILL
+    return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+}
+
+}  // namespace
+}  // namespace cvh
+
+extern "C" int cvh_paged_attention_fp8_prefill(void* out, const void* q, const uint8_t* k_cache,
+                                               const uint8_t* v_cache, const float* k_scale, const float* v_scale,
+                                               const int64_t* block_tables, int64_t table_width,
+                                               const int64_t* token_seq, const int64_t* token_kv_len,
+                                               int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                               int block_size, int scale_mode, double scale, cvh_stream_t stream) {
+    using namespace cvh;
+    if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0) return CVH_ERR_INVALID_ARG;
+    if (num_tokens == 0) return CVH_OK;
+    if (table_width == 0) return CVH_ERR_INVALID_ARG;
+    if (!out || !q || !k_cache || !v_cache || !k_scale || !v_scale || !block_tables || !token_seq || !token_kv_len)
+        return CVH_ERR_INVALID_ARG;
+    if (n_heads % n_kv_heads != 0) return CVH_ERR_INVALID_ARG;
+    const int rep = n_heads / n_kv_heads;
+    const int lg = ilog2_exact(block_size);
+    if (head_dim != kHD || lg < 4 || lg > 12 || (rep != 1 && rep != 2)) return CVH_ERR_UNSUPPORTED;
+    if (scale_mode != CVH_SCALE_PER_TOKEN_HEAD && scale_mode != CVH_SCALE_PER_TENSOR) return CVH_ERR_UNSUPPORTED;
+    if (num_tokens > (int64_t{1} << 30)) return CVH_ERR_UNSUPPORTED;
+    if (table_width > (int64_t{0x7fffffff} >> lg)) return CVH_ERR_UNSUPPORTED;    // contexts < 2^31 keys
+    auto s = reinterpret_cast<hipStream_t>(stream);
+    const float sl2 = static_cast<float>(scale) * kLog2eP;
+    auto* o = static_cast<uint16_t*>(out);
+    auto* qq = static_cast<const uint16_t*>(q);
+    const int T = static_cast<int>(num_tokens);
+    if (rep == 1) {
+        if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
+            return launch_rep<1, CVH_SCALE_PER_TOKEN_HEAD>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables,
+                                                           table_width, token_seq, token_kv_len, T, n_heads,
+                                                           n_kv_heads, lg, sl2, s);
+        return launch_rep<1, CVH_SCALE_PER_TENSOR>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables,
+                                                   table_width, token_seq, token_kv_len, T, n_heads, n_kv_heads, lg,
+                                                   sl2, s);
+    }
+    if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
+        return launch_rep<2, CVH_SCALE_PER_TOKEN_HEAD>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables,
+                                                       table_width, token_seq, token_kv_len, T, n_heads, n_kv_heads,
+                                                       lg, sl2, s);
+    return launch_rep<2, CVH_SCALE_PER_TENSOR>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables, table_width,
+                                               token_seq, token_kv_len, T, n_heads, n_kv_heads, lg, sl2, s);
+}

@@ -95,6 +95,28 @@ def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables
     check("paged_attention_fp8", code)
 
 
+def prefill_supported(n_heads: int, n_kv_heads: int, head_dim: int) -> bool:
+    """Shapes the MFMA multi-query kernel covers (else use paged_attention_fp8)."""
+    return head_dim == 128 and n_heads % n_kv_heads == 0 and n_heads // n_kv_heads in (1, 2)
+
+
+def paged_attention_fp8_prefill(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len,
+                                scale: float) -> None:
+    """paged_attention_fp8 for multi-token query rows (chunked prefill) on the MFMA kernel: same
+    arguments and result; no workspace."""
+    T = q.size(0)
+    if T == 0:
+        return
+    _require_cuda(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len)
+    H, HD = q.size(1), q.size(2)
+    BS, KV = k_cache.size(1), k_cache.size(2)
+    code = _lib.lib().cvh_paged_attention_fp8_prefill(
+        out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
+        v_scale.data_ptr(), block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(),
+        token_kv_len.data_ptr(), T, H, KV, HD, BS, _scale_mode(k_scale), float(scale), _stream(q))
+    check("paged_attention_fp8_prefill", code)
+
+
 def _rms_norm(out, x, w, eps):
     if x.size(0) == 0:
         return

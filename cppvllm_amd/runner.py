@@ -110,13 +110,20 @@ class Qwen3:
         q = torch.empty((T, H, HD), dtype=bf16, device=dev)
         att = torch.empty_like(q)
         act = torch.empty((T, I), dtype=bf16, device=dev)
+        # prompt / chunked-prefill batches (several tokens per sequence on average) take the MFMA
+        # multi-query kernel; decode rows take the stream-K decode kernel
+        S = cu_seqlens.numel() - 1
+        multi_query = not planned and T >= 2 * S and ops.prefill_supported(H, KV, HD)
         for li in range(c.n_layers):
             kc, vc, ks, vs = cache.layers[li]
             qkv = F.linear(x, self.wqkv[li])
             fused.qk_norm_rope_kv_write_fp8(q, qkv, self.q_norm[li], self.k_norm[li], self.cos, self.sin, positions,
                                             slot, kc, vc, ks, vs, None, None, H, KV, eps)
-            ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale, workspace=workspace,
-                                    planned=planned)
+            if multi_query:
+                ops.paged_attention_fp8_prefill(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale)
+            else:
+                ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
+                                        workspace=workspace, planned=planned)
             o = F.linear(att.view(T, H * HD), self.wo[li])
             fused.add_rms_norm(h, o, self.ffn_norm[li], x, eps)
             gu = F.linear(x, self.w_gate_up[li])

@@ -106,6 +106,22 @@ int cvh_paged_attention_fp8_merge_phase(void* out, const void* q, const uint8_t*
                                         int block_size, int scale_mode, double scale, int partitions,
                                         void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 
+/* Multi-token query rows on matrix cores: the same contract and result as cvh_paged_attention_fp8
+ * (same arguments; no workspace), computed by a kernel that gives 16 consecutive query tokens one
+ * K/V tile walk and runs the score and PV products on MFMA. Meant for chunked-prefill and prompt
+ * rows (several consecutive tokens of one sequence), where it reads each K/V tile once per 16
+ * tokens instead of once per token; any ragged batch is valid input (tokens of different
+ * sequences in one 16-token tile are processed one sequence at a time).
+ * Supported: head_dim 128; n_heads/n_kv_heads in {1, 2}; block_size a power of two in [16, 4096];
+ * else CVH_ERR_UNSUPPORTED (use cvh_paged_attention_fp8).
+ * Replaces the chunked-prefill route of paged_attention_fp8 (kernels/paged_attention.cu:459-473
+ * with T > S; model/model_architecture.cpp:143-147,175-176). */
+int cvh_paged_attention_fp8_prefill(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                    const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                    int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                                    int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                                    int scale_mode, double scale, cvh_stream_t stream);
+
 /* Planned launches. A decode step runs the same attention layout (block tables, token_seq,
  * token_kv_len, partition count) once per layer; cvh_paged_attention_plan builds, once, what
  * every decode workgroup would otherwise derive at the start of each launch (row prefix, token

@@ -277,6 +277,7 @@ void orc_paged_attention_fp8(uint16_t* out, const uint16_t* q, const uint8_t* k_
         const int g = (int)(u % KV);
         int64_t L = token_kv_len[t];
         if (L > table_width * BS) L = table_width * BS;
+        if (token_seq[t] < 0) L = 0;                       /* padding token (token_seq -1): zero row */
         if (L <= 0) {
             for (int r = 0; r < REP; ++r)
                 for (int d = 0; d < HD; ++d) out[(t * H + g * REP + r) * HD + d] = 0;

@@ -18,11 +18,15 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def run_gpu(b, partitions=0):
+def run_gpu(b, partitions=0, prefill=False):
     out = torch.empty_like(b["q"])
-    ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
-                            b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
-                            partitions=partitions)
+    if prefill:
+        ops.paged_attention_fp8_prefill(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                                        b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"])
+    else:
+        ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                                b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
+                                partitions=partitions)
     torch.cuda.synchronize()
     return bits(out)
 
@@ -314,3 +318,65 @@ def test_plan_shared_by_layers_config3(orc):
     rows = list(range(0, T, 16))
     cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in b.items()}
     assert_close_bf16(got1[rows], run_oracle(orc, cpu, rows=rows))
+
+
+# ---- the MFMA multi-query (chunked-prefill) kernel -------------------------------------------------
+def synth_prefill(seed, chunks, BS, H=16, KV=8, per_tensor=False, order="asc"):
+    """chunks: (context length L, query tokens n) per sequence -> the n last positions of each
+    context as consecutive query tokens (causal kv_len = pos + 1), in ascending (prefill order)
+    or descending position order."""
+    lens = [L for L, _ in chunks]
+    b = synth(seed, lens, BS, H=H, KV=KV, per_tensor=per_tensor)
+    tseq, tlen = [], []
+    for i, (L, n) in enumerate(chunks):
+        ks = range(L - n + 1, L + 1) if order == "asc" else range(L, L - n, -1)
+        for k in ks:
+            tseq.append(i)
+            tlen.append(k)
+    g = torch.Generator().manual_seed(seed + 1)
+    b["q"] = torch.randn((len(tseq), H, 128), generator=g).to(torch.bfloat16)
+    b["token_seq"] = torch.tensor(tseq, dtype=torch.int64)
+    b["token_kv_len"] = torch.tensor(tlen, dtype=torch.int64)
+    return b
+
+
+@pytest.mark.parametrize("BS", [16, 32, 256])
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_prefill_kernel_matches_oracle(orc, BS, per_tensor):
+    say(f"prefill MFMA kernel BS={BS} per_tensor={per_tensor}")
+    chunks = [(5, 5), (40, 40), (300, 300), (1000, 37), (17, 1), (700, 129), (2, 2)]
+    b = synth_prefill(51 + BS, chunks, BS, per_tensor=per_tensor)
+    assert_close_bf16(run_gpu(dev(b), prefill=True), run_oracle(orc, b))
+
+
+@pytest.mark.parametrize("H,KV", [(8, 8), (16, 8), (4, 2), (2, 1), (32, 16)])
+def test_prefill_kernel_head_layouts(orc, H, KV):
+    say(f"prefill MFMA kernel H={H} KV={KV}")
+    b = synth_prefill(61 + H + KV, [(100, 100), (333, 60), (64, 16)], 16, H=H, KV=KV)
+    assert_close_bf16(run_gpu(dev(b), prefill=True), run_oracle(orc, b))
+
+
+def test_prefill_kernel_rejects_unsupported_gqa():
+    b = dev(synth_prefill(62, [(40, 8)], 16, H=12, KV=4))
+    with pytest.raises(ops.CvhError if hasattr(ops, "CvhError") else Exception) as e:
+        run_gpu(b, prefill=True)
+    assert "UNSUPPORTED" in str(e.value)
+
+
+def test_prefill_kernel_ragged_edge_rows(orc):
+    say("prefill MFMA kernel: descending order, decode-like rows, kv_len 0 and padding rows")
+    b = synth_prefill(71, [(50, 50), (9, 1), (10, 1), (400, 3), (33, 33)], 16, order="desc")
+    # a padding row (token_seq -1) and a zero-length row: all-zero outputs
+    b["token_seq"][3] = -1
+    b["token_kv_len"][7] = 0
+    got = run_gpu(dev(b), prefill=True)
+    want = run_oracle(orc, b)
+    assert not got[3].any() and not got[7].any()
+    assert_close_bf16(got, want)
+
+
+def test_prefill_kernel_agrees_with_decode_kernel():
+    say("prefill MFMA kernel vs stream-K decode kernel on a 4096-token chunked batch")
+    chunks = [(1024, 1024), (2048, 1024), (3000, 1024), (600, 512), (900, 512)]
+    b = dev(synth_prefill(81, chunks, 256))
+    assert_close_bf16(run_gpu(b, prefill=True), run_gpu(b), max_abs=1.6e-2, mean_abs=1e-3)
