@@ -44,6 +44,7 @@ constexpr int kTile = 32;          // keys per tile
 constexpr int kVtStride = 40;      // bf16 per LDS row of V^T (32 keys + 8 pad): 80 bytes
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kNegHuge = -1e30f;
+constexpr int kSplits = 4;         // waves per workgroup, each walking every 4th key tile
 
 template <bool HI> __device__ __forceinline__ uint32_t pk_bf16(uint32_t w) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
@@ -68,17 +69,32 @@ __device__ __forceinline__ float sum_groups(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
-template <int REP, int SCALE_MODE, int WPG>
-__global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
+// K/V/scales of one 32-key tile as loaded (raw e4m3 words and f32 scales), so the next tile's
+// loads can be in flight while the current tile is computed.
+struct TileRaw {
+    uint4 k[2][2];        // [key block kb][chunk c]: 16 K bytes of key kb*16 + i16, d = c*64 + g*16
+    uint32_t v[4][4];     // [it][e]: 4 V bytes (d = 4*(lane%32) + 0..3) of key it*8 + (lane/32)*4 + e
+    float ks[2][4], vs[2][4];   // scales of keys kb*16 + g*4 + r
+};
+
+template <int REP, int SCALE_MODE, int NS>
+__global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
         uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
         const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
         const int64_t* __restrict__ tables, int64_t W, const int64_t* __restrict__ token_seq,
         const int64_t* __restrict__ token_kv_len, int T, int H, int KV, int lg_bs, float scale_log2) {
-    __shared__ __align__(16) uint16_t vt_all[WPG][kHD * kVtStride];
+    // LDS: per-wave V^T staging during the key loop; reused for the cross-wave combine afterwards
+    constexpr int kVtBytes = kHD * kVtStride * 2;
+    constexpr int kPartBytes = NS * 8 * 64 * 16;                 // one rb's O^T partials of all waves
+    constexpr int kLoopBytes = NS * kVtBytes;
+    __shared__ __align__(16) char lds[kLoopBytes > kPartBytes ? kLoopBytes : kPartBytes];
+    __shared__ __align__(16) uint16_t q_lds[REP][kQTok][kHD];    // the tile's q rows, shared by the waves
+    __shared__ float ml_lds[NS][REP][2][kQTok];                  // per wave: running max and sum per row
+
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    uint16_t* vt = vt_all[w];
-    const int kvh = blockIdx.y * WPG + w;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // key split of this wave
+    uint16_t* vt = reinterpret_cast<uint16_t*>(lds + w * kVtBytes);
+    const int kvh = blockIdx.y;
     const int t0 = blockIdx.x * kQTok;
     const int g = lane >> 4, i16 = lane & 15;
     const int BS = 1 << lg_bs, bs_mask = BS - 1;
@@ -94,20 +110,16 @@ __global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
         if (kvl > (W << lg_bs)) kvl = W << lg_bs;        // contexts end at the table's last block
     }
 
-    // Q as the B operand of S^T: step s = 2c + h covers d = c*64 + g*16 + h*8 + 0..7
-    bf16x8_t qop[REP][4];
-#pragma unroll
-    for (int rb = 0; rb < REP; ++rb) {
-        const uint16_t* qr = q + (static_cast<int64_t>(tq < T ? tq : 0) * H + kvh * REP + rb) * kHD;
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint4 v = make_uint4(0, 0, 0, 0);
-                if (tq < T) v = *reinterpret_cast<const uint4*>(qr + c * 64 + g * 16 + h * 8);
-                qop[rb][2 * c + h] = __builtin_bit_cast(bf16x8_t, v);
-            }
+    // q of the 16 tokens x REP heads into LDS (16 bytes per thread per pass)
+    for (int i = threadIdx.x; i < REP * kQTok * (kHD / 8); i += 64 * NS) {
+        const int c8 = i % (kHD / 8), row = i / (kHD / 8);
+        const int rb = row / kQTok, tk = row % kQTok;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (t0 + tk < T)
+            v = *reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(t0 + tk) * H + kvh * REP + rb) * kHD + c8 * 8);
+        *reinterpret_cast<uint4*>(&q_lds[rb][tk][c8 * 8]) = v;
     }
+    __syncthreads();
 
     f32x4_t o[REP][8];
     float m[REP], lsum[REP];
@@ -138,93 +150,100 @@ __global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
         const int64_t* trow = tables + rseq * W;
         const int row_kvl = in_run ? static_cast<int>(kvl) : 0;
 
-        for (int kb0 = 0; kb0 < kmax; kb0 += kTile) {
-            // physical blocks of the tile's keys (one block when BS >= 32; two when BS == 16)
-            // (a negative entry inside a context is invalid input: its keys read as zeros)
-            const int64_t blk0 = trow[kb0 >> lg_bs];
-            const int64_t blk1 = (BS < kTile && kb0 + 16 < kmax) ? trow[(kb0 + 16) >> lg_bs] : blk0;
-            auto blk_of = [&](int key) -> int64_t { return (BS < kTile && key >= 16) ? blk1 : blk0; };
-            auto live = [&](int key) -> bool { return kb0 + key < kmax && blk_of(key) >= 0; };
-            auto slot_of = [&](int key) -> int64_t {       // key offset inside the tile
-                return (blk_of(key) << lg_bs) + ((kb0 + key) & bs_mask);
-            };
-
-            // ---- K (A operand, rows = keys kb*16 + i16): 16 contiguous bytes per chunk c
-            bf16x8_t kop[2][4];
+        // load one tile's raw K/V/scales (keys >= kmax and negative table entries read as zeros;
+        // a negative entry inside a context is invalid input)
+        auto load_tile = [&](int kb0, TileRaw& r) {
+            // the tile's keys are two runs of 16 consecutive slots (one block when BS >= 32), so
+            // every address is a wave-uniform base plus a 32-bit lane offset
+            const bool any = kb0 < kmax;
+            const int64_t blk0 = any ? trow[kb0 >> lg_bs] : -1;
+            const int64_t blk1 = BS < kTile ? (kb0 + 16 < kmax ? trow[(kb0 + 16) >> lg_bs] : -1) : blk0;
+            const int64_t slot0 = (blk0 << lg_bs) + (kb0 & bs_mask);
+            const int64_t slot1 = BS < kTile ? (blk1 << lg_bs) + ((kb0 + 16) & bs_mask) : slot0 + 16;
+            const uint8_t* kb_ptr[2] = {kc + slot0 * row_bytes + kvh * kHD, kc + slot1 * row_bytes + kvh * kHD};
+            const uint8_t* vb_ptr[2] = {vc + slot0 * row_bytes + kvh * kHD, vc + slot1 * row_bytes + kvh * kHD};
+            const bool ok[2] = {blk0 >= 0, blk1 >= 0};
+            const uint32_t rb32 = static_cast<uint32_t>(row_bytes);
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const int key = kb * 16 + i16;
-                uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
-                if (live(key)) {
-                    const uint8_t* kr = kc + slot_of(key) * row_bytes + kvh * kHD + g * 16;
-                    c0 = *reinterpret_cast<const uint4*>(kr);
-                    c1 = *reinterpret_cast<const uint4*>(kr + 64);
-                }
-                kop[kb][0] = fp8x8_to_bf16(c0.x, c0.y);
-                kop[kb][1] = fp8x8_to_bf16(c0.z, c0.w);
-                kop[kb][2] = fp8x8_to_bf16(c1.x, c1.y);
-                kop[kb][3] = fp8x8_to_bf16(c1.z, c1.w);
-            }
-            // ---- V: 4 keys x 4 d bytes per lane per iteration, transposed into LDS as bf16
-            uint32_t vw[4][4];
-            {
-                const int c = lane & 31, kg = lane >> 5;
-#pragma unroll
-                for (int it = 0; it < 4; ++it) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int key = it * 8 + kg * 4 + e;
-                        vw[it][e] = 0u;
-                        if (live(key))
-                            vw[it][e] = *reinterpret_cast<const uint32_t*>(vc + slot_of(key) * row_bytes + kvh * kHD +
-                                                                           c * 4);
-                    }
+                r.k[kb][0] = r.k[kb][1] = make_uint4(0, 0, 0, 0);
+                if (ok[kb] && kb0 + kb * 16 + i16 < kmax) {
+                    const uint8_t* kr = kb_ptr[kb] + (static_cast<uint32_t>(i16) * rb32 + static_cast<uint32_t>(g * 16));
+                    r.k[kb][0] = *reinterpret_cast<const uint4*>(kr);
+                    r.k[kb][1] = *reinterpret_cast<const uint4*>(kr + 64);
                 }
             }
-            // ---- scales of the 4 keys g*4 + r of each 16-key block (S^T output rows)
-            float ks4[2][4], vs4[2][4];
+            const int c = lane & 31, kg = lane >> 5;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int h = it >> 1;                           // keys it*8 + ... are in half h
+                const uint8_t* vr = vb_ptr[h] + (static_cast<uint32_t>((it & 1) * 8 + kg * 4) * rb32 +
+                                                 static_cast<uint32_t>(c * 4));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int key = it * 8 + kg * 4 + e;
+                    r.v[it][e] = (ok[h] && kb0 + key < kmax) ? *reinterpret_cast<const uint32_t*>(vr + e * rb32) : 0u;
+                }
+            }
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const int key = kb * 16 + g * 4;
                 if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
                     float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-                    if (live(key)) {
-                        const int64_t si = ((blk_of(key) * KV + kvh) << lg_bs) + ((kb0 + key) & bs_mask);
-                        a = *reinterpret_cast<const float4*>(ksc + si);
-                        b = *reinterpret_cast<const float4*>(vsc + si);
+                    if (ok[kb] && kb0 + key < kmax) {
+                        const int64_t blk = kb ? blk1 : blk0;
+                        const int64_t sb = ((blk * KV + kvh) << lg_bs) + ((kb0 + kb * 16) & bs_mask);
+                        a = *reinterpret_cast<const float4*>(ksc + sb + g * 4);
+                        b = *reinterpret_cast<const float4*>(vsc + sb + g * 4);
                     }
-                    ks4[kb][0] = a.x; ks4[kb][1] = a.y; ks4[kb][2] = a.z; ks4[kb][3] = a.w;
-                    vs4[kb][0] = b.x; vs4[kb][1] = b.y; vs4[kb][2] = b.z; vs4[kb][3] = b.w;
+                    r.ks[kb][0] = a.x; r.ks[kb][1] = a.y; r.ks[kb][2] = a.z; r.ks[kb][3] = a.w;
+                    r.vs[kb][0] = b.x; r.vs[kb][1] = b.y; r.vs[kb][2] = b.z; r.vs[kb][3] = b.w;
                 } else {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        ks4[kb][r] = ks_tensor;
-                        vs4[kb][r] = vs_tensor;
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const bool lv = ok[kb] && kb0 + key + rr < kmax;
+                        r.ks[kb][rr] = lv ? ks_tensor : 0.f;
+                        r.vs[kb][rr] = lv ? vs_tensor : 0.f;
                     }
                 }
             }
+        };
 
-            // ---- S^T = K . Q^T
+        TileRaw cur, nxt;
+        int kb0 = w * kTile;
+        load_tile(kb0, cur);
+        for (; kb0 < kmax; kb0 += NS * kTile) {
+
+            // ---- S^T = K . Q^T (K e4m3 -> bf16 per step; Q from LDS)
             f32x4_t s[2][REP];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int rb = 0; rb < REP; ++rb) {
+                bf16x8_t qb[4];
 #pragma unroll
-                for (int rb = 0; rb < REP; ++rb) {
+                for (int st = 0; st < 4; ++st)
+                    qb[st] = __builtin_bit_cast(
+                            bf16x8_t, *reinterpret_cast<const uint4*>(&q_lds[rb][i16][(st >> 1) * 64 + g * 16 + (st & 1) * 8]));
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
                     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int st = 0; st < 4; ++st)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[kb][st], qop[rb][st], acc, 0, 0, 0);
+                    for (int st = 0; st < 4; ++st) {
+                        const uint4 kw = cur.k[kb][st >> 1];
+                        const bf16x8_t ka = (st & 1) ? fp8x8_to_bf16(kw.z, kw.w) : fp8x8_to_bf16(kw.x, kw.y);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[st], acc, 0, 0, 0);
+                    }
                     s[kb][rb] = acc;
                 }
+            }
 
-            // ---- V^T into LDS (previous tile's reads were issued before these writes; LDS
-            //      operations of a wave complete in order)
+            // ---- V^T into this wave's LDS region (the previous tile's reads were issued before
+            //      these writes; a wave's LDS operations complete in order)
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             {
                 const int c = lane & 31, kg = lane >> 5;
 #pragma unroll
                 for (int it = 0; it < 4; ++it) {
-                    const uint32_t w0 = vw[it][0], w1 = vw[it][1], w2 = vw[it][2], w3 = vw[it][3];
+                    const uint32_t w0 = cur.v[it][0], w1 = cur.v[it][1], w2 = cur.v[it][2], w3 = cur.v[it][3];
                     const uint32_t a = __builtin_amdgcn_perm(w1, w0, 0x05010400u);   // w0b0 w1b0 w0b1 w1b1
                     const uint32_t b = __builtin_amdgcn_perm(w1, w0, 0x07030602u);   // w0b2 w1b2 w0b3 w1b3
                     const uint32_t cc = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
@@ -242,6 +261,9 @@ __global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // this tile's K/V words are consumed: the next tile's loads go out now and stay in
+            // flight through the softmax and PV products
+            load_tile(kb0 + NS * kTile, nxt);
 
             // ---- scores, mask, online softmax (one query row per lane column)
 #pragma unroll
@@ -252,7 +274,7 @@ __global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int key = kb0 + kb * 16 + g * 4 + r;
-                        float sv = s[kb][rb][r] * (ks4[kb][r] * scale_log2);
+                        float sv = s[kb][rb][r] * (cur.ks[kb][r] * scale_log2);
                         sv = key < row_kvl ? sv : -INFINITY;
                         s[kb][rb][r] = sv;
                         mt = fmaxf(mt, sv);
@@ -270,7 +292,7 @@ __global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
                         const float p0 = __builtin_amdgcn_exp2f(s[kb][rb][r] - mn);
                         const float p1 = __builtin_amdgcn_exp2f(s[kb][rb][r + 1] - mn);
                         ps += p0 + p1;
-                        pp[kb * 2 + r / 2] = pack_bf16x2(p0 * vs4[kb][r], p1 * vs4[kb][r + 1]);
+                        pp[kb * 2 + r / 2] = pack_bf16x2(p0 * cur.vs[kb][r], p1 * cur.vs[kb][r + 1]);
                     }
                 lsum[rb] = lsum[rb] * alpha + ps;
 #pragma unroll
@@ -287,20 +309,55 @@ __global__ __launch_bounds__(64 * WPG) void paged_prefill_kernel(
                                                                        o[rb][j], 0, 0, 0);
                 }
             }
+            cur = nxt;
         }
     }
 
-    if (tq >= T) return;
+    // ---- combine the NS key splits: row max and sum per wave, then O^T partials one rb at a time;
+    //      wave w finishes d blocks [w*8/NS, (w+1)*8/NS) of every row
 #pragma unroll
     for (int rb = 0; rb < REP; ++rb) {
         const float l = sum_groups(lsum[rb]);
-        const float inv = l > 0.f ? 1.0f / l : 0.f;
-        uint16_t* orow = out + (static_cast<int64_t>(tq) * H + kvh * REP + rb) * kHD;
+        if (g == 0) {
+            ml_lds[w][rb][0][i16] = m[rb];
+            ml_lds[w][rb][1][i16] = l;
+        }
+    }
+    __syncthreads();                         // every wave is past its key loop: V^T area is free
+    float fs[REP][NS], inv[REP];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint2 v = make_uint2(pack_bf16x2(o[rb][j][0] * inv, o[rb][j][1] * inv),
-                                       pack_bf16x2(o[rb][j][2] * inv, o[rb][j][3] * inv));
-            *reinterpret_cast<uint2*>(orow + j * 16 + g * 4) = v;
+    for (int rb = 0; rb < REP; ++rb) {
+        float mx = kNegHuge;
+#pragma unroll
+        for (int x = 0; x < NS; ++x) mx = fmaxf(mx, ml_lds[x][rb][0][i16]);
+        float l = 0.f;
+#pragma unroll
+        for (int x = 0; x < NS; ++x) {
+            fs[rb][x] = __builtin_amdgcn_exp2f(ml_lds[x][rb][0][i16] - mx);
+            l += fs[rb][x] * ml_lds[x][rb][1][i16];
+        }
+        inv[rb] = l > 0.f ? 1.0f / l : 0.f;
+    }
+    f32x4_t* part = reinterpret_cast<f32x4_t*>(lds);     // [NS][8][64] per rb
+    constexpr int kJPer = 8 / NS;
+#pragma unroll
+    for (int rb = 0; rb < REP; ++rb) {
+        if (rb) __syncthreads();             // the previous rb's partials have been read
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part[(w * 8 + j) * 64 + lane] = o[rb][j];
+        __syncthreads();
+        if (tq < T) {
+            uint16_t* orow = out + (static_cast<int64_t>(tq) * H + kvh * REP + rb) * kHD;
+#pragma unroll
+            for (int jj = 0; jj < kJPer; ++jj) {
+                const int j = w * kJPer + jj;
+                f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int x = 0; x < NS; ++x) acc += part[(x * 8 + j) * 64 + lane] * fs[rb][x];
+                acc *= inv[rb];
+                const uint2 v = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+                *reinterpret_cast<uint2*>(orow + j * 16 + g * 4) = v;
+            }
         }
     }
 }
@@ -317,14 +374,8 @@ int launch_rep(uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_
                const float* vs, const int64_t* tables, int64_t W, const int64_t* tseq, const int64_t* tkvl, int T,
                int H, int KV, int lg, float sl2, hipStream_t s) {
     const unsigned gx = static_cast<unsigned>((T + kQTok - 1) / kQTok);
-#define CVH_PREFILL(WPG)                                                                                      \
-    paged_prefill_kernel<REP, SM, WPG><<<dim3(gx, KV / (WPG)), 64 * (WPG), 0, s>>>(out, q, kc, vc, ks, vs, tables, \
-                                                                                   W, tseq, tkvl, T, H, KV, lg, sl2)
-    if (KV % 8 == 0) CVH_PREFILL(8);
-    else if (KV % 4 == 0) CVH_PREFILL(4);
-    else if (KV % 2 == 0) CVH_PREFILL(2);
-    else CVH_PREFILL(1);
-#undef CVH_PREFILL
+    paged_prefill_kernel<REP, SM, kSplits><<<dim3(gx, KV), 64 * kSplits, 0, s>>>(out, q, kc, vc, ks, vs, tables, W,
+                                                                                tseq, tkvl, T, H, KV, lg, sl2);
     return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
 }
 

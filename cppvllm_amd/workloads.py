@@ -161,6 +161,38 @@ def config4(device="cpu", per_tensor=False, seed=1004, shared_prefix=False):
                         shared_prefix_blocks=8 if shared_prefix else 0)
 
 
+def prefill_lens(seed: int = 1005, T: int = 4096) -> list[int]:
+    """Prompt lengths U{100..1024} (config 5's inputs) filling one T-token prefill step; the last
+    prompt is cut so that the lengths sum to T (the engine's token budget, scheduler.cpp:60-80)."""
+    g = _cpu_gen(seed)
+    lens = []
+    while sum(lens) < T:
+        lens.append(int(torch.randint(100, 1025, (1,), generator=g)))
+    lens[-1] -= sum(lens) - T
+    return lens
+
+
+def prefill_batch(lens: list[int], bs: int, seed: int, device="cpu"):
+    """One fresh-prefill step: every position of every prompt is a query token (causal
+    kv_len = pos + 1), K/V of the whole prompts already in the cache."""
+    b = decode_batch(lens, bs, seed, device)
+    tseq, tlen = [], []
+    for i, L in enumerate(lens):
+        tseq += [i] * L
+        tlen += list(range(1, L + 1))
+    T = len(tseq)
+    dg = _dev_gen(seed + 2, device)
+    b["q"] = torch.randn((T, H, HD), generator=dg, device=device, dtype=torch.float32).to(torch.bfloat16)
+    b["token_seq"] = torch.tensor(tseq, dtype=torch.int64).to(device)
+    b["token_kv_len"] = torch.tensor(tlen, dtype=torch.int64).to(device)
+    return b
+
+
+def attention_flops(kv_lens, n_heads=H, hd=HD) -> int:
+    """q.k and p.v multiply-adds of every (query token, head, key): 4*hd flop per key and head."""
+    return int(sum(kv_lens)) * n_heads * hd * 4
+
+
 def attention_bytes(kv_lens, n_kv=KV, hd=HD, n_heads=H, per_tensor=False) -> int:
     """Algorithmic HBM bytes of one paged-attention call: every context key's K and V row of each
     kv head (+ 8 B of scales per (key, head) in per-token mode), plus q in and out (bf16)."""
