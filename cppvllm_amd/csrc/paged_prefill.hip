@@ -41,7 +41,13 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kHD = 128;
 constexpr int kQTok = 16;          // query tokens per wave
 constexpr int kTile = 32;          // keys per tile
-constexpr int kVtStride = 40;      // bf16 per LDS row of V^T (32 keys + 8 pad): 80 bytes
+// LDS row strides chosen against bank conflicts (64 banks of 4 bytes):
+//  * V^T rows are 17 dwords (32 keys + 2 pad bf16): the writers (lane c -> row 4c + e) land on
+//    banks 4*17*c mod 64, 16 distinct 2-dword slots per 16 lanes; accessed as dword pairs
+//    (ds_write2/ds_read2_b32), since odd rows are only 4-byte aligned;
+//  * q rows are 136 bf16 (272 bytes): the 16 rows read by one 16-byte load land 4 banks apart.
+constexpr int kVtStride = 34;      // bf16 per LDS row of V^T
+constexpr int kQStride = kHD + 8;  // bf16 per LDS row of q
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kNegHuge = -1e30f;
 constexpr int kSplits = 4;         // waves per workgroup, each walking every 4th key tile
@@ -56,8 +62,10 @@ __device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_p));
 }
 
 __device__ __forceinline__ float max_groups(float v) {   // max over the 4 lane groups (lanes l, l^16, l^32, l^48)
@@ -88,7 +96,7 @@ __global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
     constexpr int kPartBytes = NS * 8 * 64 * 16;                 // one rb's O^T partials of all waves
     constexpr int kLoopBytes = NS * kVtBytes;
     __shared__ __align__(16) char lds[kLoopBytes > kPartBytes ? kLoopBytes : kPartBytes];
-    __shared__ __align__(16) uint16_t q_lds[REP][kQTok][kHD];    // the tile's q rows, shared by the waves
+    __shared__ __align__(16) uint16_t q_lds[REP][kQTok][kQStride];    // the tile's q rows, shared by the waves
     __shared__ float ml_lds[NS][REP][2][kQTok];                  // per wave: running max and sum per row
 
     const int lane = threadIdx.x & 63;
@@ -110,17 +118,6 @@ __global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
         if (kvl > (W << lg_bs)) kvl = W << lg_bs;        // contexts end at the table's last block
     }
 
-    // q of the 16 tokens x REP heads into LDS (16 bytes per thread per pass)
-    for (int i = threadIdx.x; i < REP * kQTok * (kHD / 8); i += 64 * NS) {
-        const int c8 = i % (kHD / 8), row = i / (kHD / 8);
-        const int rb = row / kQTok, tk = row % kQTok;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (t0 + tk < T)
-            v = *reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(t0 + tk) * H + kvh * REP + rb) * kHD + c8 * 8);
-        *reinterpret_cast<uint4*>(&q_lds[rb][tk][c8 * 8]) = v;
-    }
-    __syncthreads();
-
     f32x4_t o[REP][8];
     float m[REP], lsum[REP];
 #pragma unroll
@@ -135,6 +132,7 @@ __global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
     const float vs_tensor = SCALE_MODE == CVH_SCALE_PER_TENSOR ? vsc[0] : 0.f;
 
     // runs of equal sequence among the 16 tokens (lanes 0..15 carry the rows)
+    bool q_staged = false;
     uint64_t todo = __builtin_amdgcn_ballot_w64(lane < kQTok && kvl > 0);
     while (todo) {
         const int leader = __builtin_ctzll(todo);
@@ -212,6 +210,22 @@ __global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
         TileRaw cur, nxt;
         int kb0 = w * kTile;
         load_tile(kb0, cur);
+        if (!q_staged) {
+            // q of the 16 tokens x REP heads into LDS (16 bytes per thread per pass), issued after
+            // the first tile's loads so the two round trips overlap. Runs are the same for every
+            // wave of the workgroup, so this barrier is reached uniformly.
+            for (int i = threadIdx.x; i < REP * kQTok * (kHD / 8); i += 64 * NS) {
+                const int c8 = i % (kHD / 8), row = i / (kHD / 8);
+                const int rb = row / kQTok, tk = row % kQTok;
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (t0 + tk < T)
+                    v = *reinterpret_cast<const uint4*>(q + (static_cast<int64_t>(t0 + tk) * H + kvh * REP + rb) * kHD +
+                                                        c8 * 8);
+                *reinterpret_cast<uint4*>(&q_lds[rb][tk][c8 * 8]) = v;
+            }
+            __syncthreads();
+            q_staged = true;
+        }
         for (; kb0 < kmax; kb0 += NS * kTile) {
 
             // ---- S^T = K . Q^T (K e4m3 -> bf16 per step; Q from LDS)
@@ -255,8 +269,9 @@ __global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
                     const int key = it * 8 + kg * 4;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const uint2 v2 = make_uint2(pk_bf16<false>(tr[e]), pk_bf16<true>(tr[e]));
-                        *reinterpret_cast<uint2*>(vt + (c * 4 + e) * kVtStride + key) = v2;
+                        uint32_t* dst = reinterpret_cast<uint32_t*>(vt + (c * 4 + e) * kVtStride + key);
+                        dst[0] = pk_bf16<false>(tr[e]);
+                        dst[1] = pk_bf16<true>(tr[e]);
                     }
                 }
             }
@@ -295,16 +310,17 @@ __global__ __launch_bounds__(64 * NS, 2) void paged_prefill_kernel(
                         pp[kb * 2 + r / 2] = pack_bf16x2(p0 * cur.vs[kb][r], p1 * cur.vs[kb][r + 1]);
                     }
                 lsum[rb] = lsum[rb] * alpha + ps;
+                if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {     // wave-uniform: the max moved
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
+                    for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
+                }
                 const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pp);
                 // ---- O^T += V^T . P^T over the 8 d blocks
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint16_t* vr = vt + (j * 16 + i16) * kVtStride + g * 4;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-                    const uint32_t va[4] = {lo.x, lo.y, hi.x, hi.y};
+                    const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vr);
+                    const uint32_t va[4] = {v32[0], v32[1], v32[8], v32[9]};
                     o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pop,
                                                                        o[rb][j], 0, 0, 0);
                 }
