@@ -11,8 +11,10 @@
 //                                    budget and a per-sequence chunk cap, preemption by recompute
 //                                    of the most recently admitted, then FIFO admission)
 //   * step groups                    engine/model_runner.cpp:147-196
-// The step here is synchronous: a scheduled step is post-processed before the next is built, so
-// the reference's two-deep launch ring and its pending-token feedback are not needed.
+//   * two-deep launch ring           engine/llm_engine.cpp:70-113 (a step may be scheduled while
+//                                    the previous one is still running: its sampled tokens are
+//                                    placeholders the runner feeds on the device, batch.feed_src)
+// A caller may also run steps synchronously (schedule, then postprocess, then schedule ...).
 #include "../../include/cppvllm_engine.h"
 
 #include <algorithm>
@@ -41,7 +43,9 @@ struct Seq {
     int64_t num_prompt = 0;
     int64_t num_cached = 0;            // tokens whose K/V are in the cache
     int64_t num_sched = 0;             // tokens scheduled in the step being built
-    int64_t sample_at = -1;            // token index sampled by the last step, -1 = none
+    int32_t inflight = 0;              // scheduled steps containing this sequence, not yet post-processed
+    int64_t last_row = -1;             // its row in the newest scheduled step, if that step samples it
+    bool done = false;                 // finished; its blocks are released once inflight == 0
 
     int64_t size() const { return static_cast<int64_t>(tokens.size()); }
     int64_t completion() const { return size() - num_prompt; }
@@ -212,29 +216,33 @@ public:
     }
 
     int schedule(cve_batch* out) {
-        if (has_batch_) return CVE_ERR_STATE;
-        std::vector<Seq*> picked = pick();
+        if (flights_.size() >= kMaxFlights) return CVE_ERR_STATE;
+        // preemption releases blocks, which is only safe when no scheduled step can still touch them
+        std::vector<Seq*> picked = pick(/*allow_preempt=*/flights_.empty());
         if (picked.empty()) {
             *out = cve_batch{};
+            if (!flights_.empty()) return CVE_ERR_BUSY;
             return (waiting_.empty() && running_.empty()) ? CVE_OK : CVE_ERR_EMPTY;
         }
         build(picked, out);
-        has_batch_ = true;
         ++stats_.steps;
         return CVE_OK;
     }
 
+    // Accept the sampled tokens of the oldest scheduled step (scheduler.cpp:121-154).
     int postprocess(const int64_t* sampled, int64_t n) {
-        if (!has_batch_) return CVE_ERR_STATE;
-        if (n != static_cast<int64_t>(batch_.size()) || (n > 0 && !sampled)) return CVE_ERR_INVALID_ARG;
+        if (flights_.empty()) return CVE_ERR_STATE;
+        Flight& f = flights_.front();
+        if (n != static_cast<int64_t>(f.seqs.size()) || (n > 0 && !sampled)) return CVE_ERR_INVALID_ARG;
         for (int64_t j = 0; j < n; ++j) {
-            Seq* s = batch_[j];
-            if (s->sample_at < 0) {            // a prefill chunk that does not reach the end
+            Seq* s = f.seqs[j];
+            --s->inflight;
+            const int64_t at = f.at[j];
+            if (s->done) continue;               // finished by an older step: a dropped extra token
+            if (at < 0) {                        // a prefill chunk that does not reach the end
                 bm_.commit(*s);
                 continue;
             }
-            const int64_t at = s->sample_at;
-            s->sample_at = -1;
             const int32_t tok = static_cast<int32_t>(sampled[j]);
             s->tokens[at] = tok;
             ++stats_.tokens_sampled;
@@ -242,23 +250,26 @@ public:
             const bool len = at + 1 - s->num_prompt >= s->max_tokens;
             bm_.commit(*s);
             if (eos || len) {
-                s->tokens.resize(static_cast<size_t>(at) + 1);
+                s->tokens.resize(static_cast<size_t>(at) + 1);   // drops a newer step's placeholder
+                s->done = true;
                 s->state = State::kFinished;
-                bm_.release(*s);
                 finish(s);
             }
         }
         running_.erase(std::remove_if(running_.begin(), running_.end(),
                                       [](const Seq* s) { return s->state == State::kFinished; }),
                        running_.end());
-        for (Seq* s : batch_)
-            if (s->state == State::kFinished) live_.erase(s->id);   // frees s
-        batch_.clear();
-        has_batch_ = false;
+        std::vector<Seq*> seqs = std::move(f.seqs);
+        flights_.pop_front();
+        for (Seq* s : seqs)
+            if (s->done && s->inflight == 0 && s->table.size() > 0) bm_.release(*s);
+        for (Seq* s : seqs)
+            if (s->done && s->inflight == 0) live_.erase(s->id);   // frees s (duplicates: find fails)
         return CVE_OK;
     }
 
-    bool finished() const { return waiting_.empty() && running_.empty(); }
+    bool finished() const { return waiting_.empty() && running_.empty() && flights_.empty(); }
+    int64_t inflight() const { return static_cast<int64_t>(flights_.size()); }
     cve_stats stats() const {
         cve_stats s = stats_;
         s.free_blocks = bm_.num_free();
@@ -275,7 +286,7 @@ public:
 
 private:
     // Which sequences run this step and how many tokens each (scheduler.cpp:37-103).
-    std::vector<Seq*> pick() {
+    std::vector<Seq*> pick(bool allow_preempt) {
         int64_t budget = cfg_.max_num_batched_tokens;
         const int64_t cap = cfg_.max_chunk_tokens > 0 ? cfg_.max_chunk_tokens : INT64_MAX;
         std::vector<Seq*> out;
@@ -285,8 +296,15 @@ private:
         while (!pending.empty()) {
             Seq* s = pending.front();
             pending.pop_front();
-            const int64_t want = std::min({s->uncached(), budget, cap});
+            // a sequence whose last sample (possibly still in flight) completes max_tokens has
+            // nothing more to run
+            const bool complete = s->inflight > 0 && s->completion() >= s->max_tokens;
+            const int64_t want = complete ? 0 : std::min({s->uncached(), budget, cap});
             if (want <= 0 || static_cast<int64_t>(out.size()) >= cfg_.max_num_seqs) {
+                kept.push_back(s);
+                continue;
+            }
+            if (!allow_preempt && !bm_.can_append(*s)) {   // wait for the ring to drain
                 kept.push_back(s);
                 continue;
             }
@@ -307,6 +325,7 @@ private:
             kept.push_back(s);
         }
         running_ = std::move(kept);
+        // new requests are admitted whatever is in flight (admission only takes free blocks)
         while (!preempted && !waiting_.empty() && budget > 0 &&
                static_cast<int64_t>(running_.size()) < cfg_.max_num_seqs) {
             Seq* s = waiting_.front();
@@ -340,21 +359,24 @@ private:
     // Flat batch of the step, ordered by group, then the launch bookkeeping of
     // scheduler.cpp:105-119 (cached count advances, a sampling row reserves its token slot).
     void build(const std::vector<Seq*>& picked, cve_batch* out) {
-        batch_.clear();
+        flights_.emplace_back();
+        Flight& f = flights_.back();
+        std::vector<Seq*>& rows = f.seqs;
         int64_t gs[CVE_NUM_GROUPS + 1] = {0, 0, 0, 0};
         for (int g = 0; g < CVE_NUM_GROUPS; ++g) {
-            gs[g] = static_cast<int64_t>(batch_.size());
+            gs[g] = static_cast<int64_t>(rows.size());
             for (Seq* s : picked)
-                if (group_of(*s) == g) batch_.push_back(s);
+                if (group_of(*s) == g) rows.push_back(s);
         }
-        gs[CVE_NUM_GROUPS] = static_cast<int64_t>(batch_.size());
+        gs[CVE_NUM_GROUPS] = static_cast<int64_t>(rows.size());
         const int64_t S = gs[CVE_NUM_GROUPS];
         int64_t T = 0, W = 1;
-        for (Seq* s : batch_) {
+        for (Seq* s : rows) {
             T += s->num_sched;
             W = std::max(W, ceil_div(s->num_cached + s->num_sched, cfg_.block_size));
         }
         tokens_.assign(T, 0);
+        feed_.assign(T, -1);
         positions_.assign(T, 0);
         cu_.assign(S + 1, 0);
         kv_.assign(S, 0);
@@ -363,11 +385,14 @@ private:
         ids_.assign(S, 0);
         int64_t t = 0;
         for (int64_t j = 0; j < S; ++j) {
-            Seq* s = batch_[j];
+            Seq* s = rows[j];
             const int64_t c = s->num_cached, q = s->num_sched, kv = c + q;
             for (int64_t k = 0; k < q; ++k, ++t) {
                 tokens_[t] = s->tokens[c + k];
                 positions_[t] = c + k;
+                // a placeholder is being sampled by the previous (still running) step: the runner
+                // copies it on the device from that step's sampled row
+                if (tokens_[t] == kPending) feed_[t] = s->last_row;
             }
             cu_[j + 1] = t;
             kv_[j] = kv;
@@ -377,10 +402,10 @@ private:
             samples_[j] = samples ? 1 : 0;
             s->num_cached = kv;
             s->num_sched = 0;
-            if (samples) {
-                s->sample_at = s->size();
-                s->tokens.push_back(kPending);
-            }
+            ++s->inflight;
+            f.at.push_back(samples ? s->size() : -1);
+            s->last_row = samples ? j : -1;
+            if (samples) s->tokens.push_back(kPending);
             stats_.tokens_scheduled += q;
         }
         out->num_seqs = S;
@@ -394,6 +419,7 @@ private:
         out->block_tables = tables_.data();
         out->samples = samples_.data();
         out->seq_ids = ids_.data();
+        out->feed_src = feed_.data();
     }
     void finish(Seq* s) {
         Output o;
@@ -409,11 +435,15 @@ private:
     std::vector<Seq*> running_;
     std::unordered_map<int64_t, std::unique_ptr<Seq>> live_;
     std::map<int64_t, Output> done_;
-    std::vector<Seq*> batch_;
-    bool has_batch_ = false;
+    struct Flight {
+        std::vector<Seq*> seqs;          // rows of the step
+        std::vector<int64_t> at;         // token index each row samples, -1 = none
+    };
+    static constexpr size_t kMaxFlights = 2;   // llm_engine.h:51 (kDepth)
+    std::deque<Flight> flights_;
     int64_t next_id_ = 0;
     cve_stats stats_{};
-    std::vector<int64_t> tokens_, positions_, cu_, kv_, tables_, ids_;
+    std::vector<int64_t> tokens_, feed_, positions_, cu_, kv_, tables_, ids_;
     std::vector<int8_t> samples_;
 };
 
@@ -445,6 +475,7 @@ int cve_postprocess(void* e, const int64_t* sampled, int64_t n) {
     return cve::E(e)->postprocess(sampled, n);
 }
 int cve_is_finished(void* e) { return e && cve::E(e)->finished() ? 1 : 0; }
+int64_t cve_num_outstanding(void* e) { return e ? cve::E(e)->inflight() : 0; }
 int cve_get_stats(void* e, cve_stats* out) {
     if (!e || !out) return CVE_ERR_INVALID_ARG;
     *out = cve::E(e)->stats();

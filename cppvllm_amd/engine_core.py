@@ -16,7 +16,7 @@ import numpy as np
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libcvh_engine.so"
 
-CVE_OK, CVE_ERR_INVALID_ARG, CVE_ERR_TOO_LONG, CVE_ERR_STATE, CVE_ERR_EMPTY = 0, -1, -2, -3, -4
+CVE_OK, CVE_ERR_INVALID_ARG, CVE_ERR_TOO_LONG, CVE_ERR_STATE, CVE_ERR_EMPTY, CVE_ERR_BUSY = 0, -1, -2, -3, -4, -5
 GROUP_DECODE, GROUP_FRESH, GROUP_CONT = 0, 1, 2
 
 
@@ -31,7 +31,8 @@ class _Batch(C.Structure):
                 ("group_start", C.c_int64 * 4), ("tokens", C.POINTER(C.c_int64)),
                 ("positions", C.POINTER(C.c_int64)), ("cu_seqlens", C.POINTER(C.c_int64)),
                 ("kv_lens", C.POINTER(C.c_int64)), ("block_tables", C.POINTER(C.c_int64)),
-                ("samples", C.POINTER(C.c_int8)), ("seq_ids", C.POINTER(C.c_int64))]
+                ("samples", C.POINTER(C.c_int8)), ("seq_ids", C.POINTER(C.c_int64)),
+                ("feed_src", C.POINTER(C.c_int64))]
 
 
 class Stats(C.Structure):
@@ -59,6 +60,7 @@ def lib() -> C.CDLL:
         "cve_schedule": (C.c_int, [vp, C.POINTER(_Batch)]),
         "cve_postprocess": (C.c_int, [vp, C.POINTER(i64), i64]),
         "cve_is_finished": (C.c_int, [vp]),
+        "cve_num_outstanding": (i64, [vp]),
         "cve_get_stats": (C.c_int, [vp, C.POINTER(Stats)]),
         "cve_num_finished": (i64, [vp]),
         "cve_finished_output": (i64, [vp, i64, C.POINTER(i64), C.POINTER(i32), i64]),
@@ -86,6 +88,7 @@ class Batch:
     samples: np.ndarray         # bool [S]
     seq_ids: np.ndarray         # int64 [S]
     group_start: tuple
+    feed_src: np.ndarray = None  # int64 [T]: row of the previous step's samples feeding a token, or -1
 
     @property
     def num_seqs(self) -> int:
@@ -100,6 +103,10 @@ def _arr(ptr, n, dtype):
     if n == 0:
         return np.zeros(0, dtype=dtype)
     return np.ctypeslib.as_array(ptr, shape=(n,)).astype(dtype, copy=True)
+
+
+class EngineBusy(RuntimeError):
+    """Nothing can be scheduled until the oldest outstanding step is post-processed."""
 
 
 class EngineCore:
@@ -127,6 +134,8 @@ class EngineCore:
     def schedule(self) -> Batch | None:
         b = _Batch()
         code = lib().cve_schedule(self._h, C.byref(b))
+        if code == CVE_ERR_BUSY:
+            raise EngineBusy("retire the oldest step first")
         if code != CVE_OK:
             raise RuntimeError(f"schedule failed ({code})")
         if b.num_seqs == 0:
@@ -136,7 +145,7 @@ class EngineCore:
                      cu_seqlens=_arr(b.cu_seqlens, S + 1, np.int64), kv_lens=_arr(b.kv_lens, S, np.int64),
                      block_tables=_arr(b.block_tables, S * W, np.int64).reshape(S, W),
                      samples=_arr(b.samples, S, np.int8).astype(bool), seq_ids=_arr(b.seq_ids, S, np.int64),
-                     group_start=tuple(int(x) for x in b.group_start))
+                     group_start=tuple(int(x) for x in b.group_start), feed_src=_arr(b.feed_src, T, np.int64))
 
     def postprocess(self, sampled) -> None:
         s = np.ascontiguousarray(sampled, dtype=np.int64)
@@ -146,6 +155,10 @@ class EngineCore:
 
     def is_finished(self) -> bool:
         return bool(lib().cve_is_finished(self._h))
+
+    def outstanding(self) -> int:
+        """Scheduled steps not yet post-processed (0..2)."""
+        return int(lib().cve_num_outstanding(self._h))
 
     def stats(self) -> Stats:
         st = Stats()

@@ -1,7 +1,8 @@
 """Request-level engine: the serving loop around the native scheduler and the model runner.
 
 Mirrors LLMEngine (engine/llm_engine.h:34-69, engine/llm_engine.cpp:30-155): ``add_request``,
-``step`` (schedule -> run -> postprocess), ``is_finished``, ``generate``, ``stats``. Scheduling
+``step`` (a two-deep ring of schedule -> launch, then collect -> postprocess), ``is_finished``,
+``generate``, ``stats``. Scheduling
 and the paged block manager are the C++ core (include/cppvllm_engine.h); the step runs on the
 gfx950 kernels through ``ModelRunner``.
 """
@@ -12,7 +13,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from .engine_core import EngineCore
+from .engine_core import EngineBusy, EngineCore
 from .runner import KVCache, ModelRunner, Qwen3, Qwen3Config
 
 
@@ -35,6 +36,7 @@ class EngineConfig:
     gpu_memory_utilization: float = 0.90
     num_kv_blocks: int = -1
     enforce_eager: bool = False
+    depth: int = 2                 # outstanding steps (llm_engine.h:51 kDepth); 1 = synchronous
     seed: int = 0
     weight_std: float = 0.02
     eos_token_id: int = 151645
@@ -57,6 +59,7 @@ class LLMEngine:
                                num_blocks=self.num_blocks, graph_max_blocks=self.runner.graph_width,
                                eos_token_id=cfg.eos_token_id)
         self.temps: dict[int, float] = {}
+        self._ring: list = []             # (batch, runner handle) of launched, unprocessed steps
 
     def _size_kv_cache(self) -> int:
         """Blocks that fit in gpu_memory_utilization of the device after the weights
@@ -81,15 +84,26 @@ class LLMEngine:
         return rid
 
     def step(self) -> int:
-        """One scheduled step; returns the number of sampled tokens."""
-        batch = self.core.schedule()
-        if batch is None:
+        """Advance the two-deep launch ring (engine/llm_engine.cpp:70-113): schedule and launch
+        the next step when fewer than two are outstanding, and post-process the oldest one once two
+        are (or when nothing else can be scheduled). Returns the number of tokens sampled by the
+        step post-processed in this call (0 if none was)."""
+        if len(self._ring) < self.cfg.depth:
+            try:
+                batch = self.core.schedule()
+            except EngineBusy:
+                batch = None
+            if batch is not None:
+                temps = None
+                if self.temps:
+                    temps = np.array([self.temps.get(int(r), 0.0) for r in batch.seq_ids], dtype=np.float32)
+                self._ring.append((batch, self.runner.launch(batch, temps)))
+                if len(self._ring) < self.cfg.depth:
+                    return 0
+        if not self._ring:
             return 0
-        temps = None
-        if self.temps:
-            temps = np.array([self.temps.get(int(r), 0.0) for r in batch.seq_ids], dtype=np.float32)
-        sampled = self.runner.run(batch, temps)
-        self.core.postprocess(sampled)
+        batch, handle = self._ring.pop(0)
+        self.core.postprocess(self.runner.collect(handle))
         return int(np.count_nonzero(batch.samples))
 
     def is_finished(self) -> bool:

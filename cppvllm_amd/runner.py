@@ -150,8 +150,16 @@ def _graph_sizes(max_batch: int) -> list[int]:
 
 
 class ModelRunner:
-    """Runs scheduled batches (cppvllm_amd.engine_core.Batch) and returns one sampled token per
-    row (-1 for rows that do not sample)."""
+    """Launches scheduled batches (cppvllm_amd.engine_core.Batch) asynchronously and collects one
+    sampled token per row (-1 for rows that do not sample).
+
+    Two launch slots alternate (the reference's two-deep ring, engine/model_runner.cpp:169-212 and
+    engine/llm_engine.cpp:70-113): each slot owns pinned host staging and a device buffer of the
+    step's sampled tokens in row order, so step N+1 can be staged and launched while step N runs,
+    reading N's samples on the device (cvh_feed_tokens) for the tokens the scheduler left as
+    placeholders. Device input buffers are shared by the slots: the stream orders their reuse.
+    A slot is reused two launches later, after collect() of its previous step has synchronised on
+    that step's completion event."""
 
     def __init__(self, model: Qwen3, cache: KVCache, *, max_num_batched_tokens: int = 4096, max_num_seqs: int = 256,
                  max_model_len: int = 4096, graph_max_blocks: int | None = None, enforce_eager: bool = False,
@@ -160,59 +168,67 @@ class ModelRunner:
         c = model.cfg
         dev = model.device
         BS = cache.block_size
-        self.max_tokens = max(max_num_batched_tokens, max_num_seqs)
-        self.max_seqs = max_num_seqs
-        self.table_width = -(-max_model_len // BS)
-        self.graph_width = graph_max_blocks or self.table_width
+        self.max_tokens = Tm = max(max_num_batched_tokens, max_num_seqs)
+        self.max_seqs = Sm = max_num_seqs
+        self.table_width = Wm = -(-max_model_len // BS)
+        self.graph_width = Wg = graph_max_blocks or self.table_width
+        self.max_graph_batch = Bm = max_num_seqs
         i64 = dict(dtype=torch.int64)
-        # pinned staging (StagedBuffer, utils/tensor.h:64-110) and device copies
-        self.h_tok = torch.empty(self.max_tokens, pin_memory=True, **i64)
-        self.h_pos = torch.empty(self.max_tokens, pin_memory=True, **i64)
-        self.h_cu = torch.empty(self.max_seqs + 1, pin_memory=True, **i64)
-        self.h_tab = torch.empty(self.max_seqs * max(self.table_width, self.graph_width), pin_memory=True, **i64)
-        self.h_out = torch.empty(self.max_tokens, pin_memory=True, **i64)
-        self.d_tok = torch.empty(self.max_tokens, device=dev, **i64)
-        self.d_pos = torch.empty(self.max_tokens, device=dev, **i64)
-        self.d_cu = torch.empty(self.max_seqs + 1, device=dev, **i64)
-        self.d_tab = torch.empty(self.max_seqs * max(self.table_width, self.graph_width), device=dev, **i64)
-        self.d_out = torch.empty(self.max_tokens, device=dev, **i64)
-        self.d_rows = torch.empty(self.max_seqs, device=dev, **i64)
-        self.h_rows = torch.empty(self.max_seqs, pin_memory=True, **i64)
-        self.h_temps = torch.empty(self.max_seqs, pin_memory=True, dtype=torch.float32)
-        self.d_temps = torch.empty(self.max_seqs, device=dev, dtype=torch.float32)
+        # decode-graph inputs, one int64 arena: tok | pos | cu | feed | tables (B x Wg)
+        self.g_off = np.cumsum([0, Bm, Bm, Bm + 1, Bm]).tolist()
+        self.g_len = self.g_off[-1] + Bm * Wg
+        self.d_garena = torch.zeros(self.g_len, device=dev, **i64)
+        o = self.g_off
+        self.g_tok, self.g_pos = self.d_garena[o[0]:o[1]], self.d_garena[o[1]:o[2]]
+        self.g_cu, self.g_feed, self.g_tab = self.d_garena[o[2]:o[3]], self.d_garena[o[3]:o[4]], self.d_garena[o[4]:]
+        # eager inputs: tok | pos | feed | cu | sampled token rows | their batch rows | tables (S x W)
+        self.e_off = np.cumsum([0, Tm, Tm, Tm, Sm + 1, Sm, Sm]).tolist()
+        self.e_len = self.e_off[-1] + Sm * Wm
+        self.d_earena = torch.zeros(self.e_len, device=dev, **i64)
+        # per launch slot: pinned staging (StagedBuffer, utils/tensor.h:64-110), sampled tokens
+        self.h_garena = [torch.zeros(self.g_len, pin_memory=True, **i64) for _ in range(2)]
+        self.h_earena = [torch.zeros(self.e_len, pin_memory=True, **i64) for _ in range(2)]
+        self.h_temps = [torch.zeros(Sm, pin_memory=True, dtype=torch.float32) for _ in range(2)]
+        self.d_temps = torch.zeros(Sm, device=dev, dtype=torch.float32)
+        self.d_sampled = [torch.zeros(Sm, device=dev, **i64) for _ in range(2)]
+        self.h_sampled = [torch.zeros(Sm, pin_memory=True, **i64) for _ in range(2)]
+        self.d_tmp = torch.zeros(Sm, device=dev, **i64)
+        self.events = [torch.cuda.Event() for _ in range(2)]
+        self.slot, self.last_slot = 0, None
         self.seed, self.sample_step = seed, 0
-        self.ws_eager = ops.paged_attention_workspace(self.max_tokens, c.n_heads, c.n_kv_heads, c.head_dim,
-                                                      self.table_width, BS, 0, dev)
+        self.ws_eager = ops.paged_attention_workspace(Tm, c.n_heads, c.n_kv_heads, c.head_dim, Wm, BS, 0, dev)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.max_graph_batch = max_num_seqs
         if not enforce_eager:
             self.capture_graphs()
 
     # ---- decode graphs -------------------------------------------------------------------------
-    def _stage_graph_rows(self, toks, pos, tables, B: int) -> None:
+    def _stage_graph_rows(self, toks, pos, tables, B: int, feed=None, slot: int = 0) -> bool:
         """Rows [0, S) are the decode rows; [S, B) are idle rows on the scratch block at position 0
-        with kv_len 1 (model_runner.cpp:327-357)."""
+        with kv_len 1 (model_runner.cpp:327-357). One host-to-device copy. Returns whether any
+        token must be fed from the previous step's samples."""
         S = len(toks)
-        Wg = self.graph_width
-        ht, hp, hc = self.h_tok.numpy(), self.h_pos.numpy(), self.h_cu.numpy()
-        tab = self.h_tab.numpy()[:B * Wg].reshape(B, Wg)
-        ht[:S], hp[:S] = toks, pos
-        ht[S:B], hp[S:B] = 0, 0
-        hc[:B + 1] = np.arange(B + 1)
+        Wg, o = self.graph_width, self.g_off
+        h = self.h_garena[slot].numpy()
+        h[o[0]:o[0] + S], h[o[1]:o[1] + S] = toks, pos
+        h[o[0] + S:o[0] + B], h[o[1] + S:o[1] + B] = 0, 0
+        h[o[2]:o[2] + B + 1] = np.arange(B + 1)
+        need_feed = feed is not None and bool((feed >= 0).any())
+        if need_feed:
+            h[o[3]:o[3] + S] = feed
+        tab = h[o[4]:o[4] + B * Wg].reshape(B, Wg)
         tab[:] = -1
         if S:
             w = min(tables.shape[1], Wg)
             tab[:S, :w] = tables[:, :w]
         tab[S:B, 0] = self.cache.scratch_block
-        self.d_tok[:B].copy_(self.h_tok[:B], non_blocking=True)
-        self.d_pos[:B].copy_(self.h_pos[:B], non_blocking=True)
-        self.d_cu[:B + 1].copy_(self.h_cu[:B + 1], non_blocking=True)
-        self.d_tab[:B * Wg].copy_(self.h_tab[:B * Wg], non_blocking=True)
+        n = o[4] + B * Wg
+        self.d_garena[:n].copy_(self.h_garena[slot][:n], non_blocking=True)
+        return need_feed
 
     def _graph_body(self, B: int, ws) -> None:
         Wg = self.graph_width
-        x = self.model.forward(self.cache, self.d_tok[:B], self.d_pos[:B], self.d_cu[:B + 1],
-                               self.d_tab[:B * Wg].view(B, Wg), ws, planned=True)
+        x = self.model.forward(self.cache, self.g_tok[:B], self.g_pos[:B], self.g_cu[:B + 1],
+                               self.g_tab[:B * Wg].view(B, Wg), ws, planned=True)
         self.g_hidden[:B].copy_(x)
 
     def capture_graphs(self) -> None:
@@ -240,85 +256,112 @@ class ModelRunner:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
 
-    def _stage_temps(self, temps, n: int):
-        if temps is None or not np.any(temps > 0):
-            return None
-        self.h_temps.numpy()[:n] = temps
-        self.d_temps[:n].copy_(self.h_temps[:n], non_blocking=True)
-        return self.d_temps[:n]
-
-    def _sample(self, x_rows, temps) -> torch.Tensor:
-        R = x_rows.size(0)
-        self.model.sample(x_rows, self.d_out[:R], self._stage_temps(temps, R), self.seed, self.sample_step)
+    # ---- sampling --------------------------------------------------------------------------------
+    def _sample(self, x_rows, out, temps_dev) -> None:
+        self.model.sample(x_rows, out, temps_dev, self.seed, self.sample_step)
         self.sample_step += 1
-        return self.d_out[:R]
 
-    def _run_graph(self, toks, pos, tables, temps) -> torch.Tensor:
-        S = len(toks)
-        B = next(b for b in sorted(self.graphs) if b >= S)
-        self._stage_graph_rows(toks, pos, tables, B)
-        self.graphs[B].replay()
-        return self._sample(self.g_hidden[:S], temps)
+    def _prev_sampled(self):
+        if self.last_slot is None:
+            raise RuntimeError("a batch feeds tokens but no step was launched before it")
+        return self.d_sampled[self.last_slot]
 
     # ---- eager ragged forward ------------------------------------------------------------------
-    def _run_eager(self, toks, pos, cu, tables, sample_rows, temps) -> torch.Tensor:
+    def _run_eager(self, toks, pos, cu, tables, sample_rows, temps_dev, feed=None, slot: int = 0, row_ids=None,
+                   out=None):
+        """One eager forward over a ragged batch; samples the token rows `sample_rows` into
+        out[row_ids] (row_ids: numpy batch rows), or into a temporary that is returned."""
         T, S = len(toks), len(cu) - 1
         W = tables.shape[1]
         if T > self.max_tokens or S > self.max_seqs or W > self.table_width:
             raise ValueError(f"batch exceeds the runner's limits (T={T}, S={S}, W={W})")
-        self.h_tok.numpy()[:T] = toks
-        self.h_pos.numpy()[:T] = pos
-        self.h_cu.numpy()[:S + 1] = cu
-        self.h_tab.numpy()[:S * W] = tables.reshape(-1)
-        self.d_tok[:T].copy_(self.h_tok[:T], non_blocking=True)
-        self.d_pos[:T].copy_(self.h_pos[:T], non_blocking=True)
-        self.d_cu[:S + 1].copy_(self.h_cu[:S + 1], non_blocking=True)
-        self.d_tab[:S * W].copy_(self.h_tab[:S * W], non_blocking=True)
-        x = self.model.forward(self.cache, self.d_tok[:T], self.d_pos[:T], self.d_cu[:S + 1],
-                               self.d_tab[:S * W].view(S, W), self.ws_eager, planned=False)
         R = len(sample_rows)
+        o = self.e_off
+        h = self.h_earena[slot].numpy()
+        h[o[0]:o[0] + T], h[o[1]:o[1] + T] = toks, pos
+        need_feed = feed is not None and bool((feed >= 0).any())
+        if need_feed:
+            h[o[2]:o[2] + T] = feed
+        h[o[3]:o[3] + S + 1] = cu
+        h[o[4]:o[4] + R] = sample_rows
+        if row_ids is not None:
+            h[o[5]:o[5] + R] = row_ids
+        h[o[6]:o[6] + S * W] = tables.reshape(-1)
+        n = o[6] + S * W
+        self.d_earena[:n].copy_(self.h_earena[slot][:n], non_blocking=True)
+        d = self.d_earena
+        tok = d[o[0]:o[0] + T]
+        if need_feed:
+            fused.feed_tokens(tok, d[o[2]:o[2] + T], self._prev_sampled())
+        x = self.model.forward(self.cache, tok, d[o[1]:o[1] + T], d[o[3]:o[3] + S + 1],
+                               d[o[6]:o[6] + S * W].view(S, W), self.ws_eager, planned=False)
         if R == 0:
-            return self.d_out[:0]
-        self.h_rows.numpy()[:R] = sample_rows
-        self.d_rows[:R].copy_(self.h_rows[:R], non_blocking=True)
-        return self._sample(x.index_select(0, self.d_rows[:R]), temps)
+            return self.d_tmp[:0]
+        rows = x.index_select(0, d[o[4]:o[4] + R])
+        self._sample(rows, self.d_tmp[:R], temps_dev)
+        if out is not None and row_ids is not None:
+            out.index_copy_(0, d[o[5]:o[5] + R], self.d_tmp[:R])
+        return self.d_tmp[:R]
 
-    def run(self, batch, temps: np.ndarray | None = None) -> np.ndarray:
-        """One step: decode rows through graphs (chunks of the largest captured size), the rest in
-        one eager ragged forward; returns the sampled token per row (-1 where none). temps: per-row
-        sampling temperature (None or <= 0: greedy)."""
+    # ---- one step ----------------------------------------------------------------------------------
+    def launch(self, batch, temps: np.ndarray | None = None):
+        """Stage and enqueue one step: decode rows through the captured graph of the smallest
+        batch size >= their count, the other rows in one eager ragged forward. Returns a handle
+        for collect(). temps: per-row sampling temperature (None or <= 0: greedy)."""
+        slot = self.slot
         S = batch.num_seqs
-        out = np.full(S, -1, dtype=np.int64)
+        if S > self.max_seqs:
+            raise ValueError(f"{S} rows > max_num_seqs {self.max_seqs}")
         d0, d1 = batch.group_start[0], batch.group_start[1]
-        pending = []   # (row indices, device tensor)
-        if self.graphs and d1 > d0:
-            cap = self.max_graph_batch
-            for a in range(d0, d1, cap):
-                b = min(d1, a + cap)
-                cu = batch.cu_seqlens
-                t0 = cu[a:b]
-                dev = self._run_graph(batch.tokens[t0], batch.positions[t0], batch.block_tables[a:b],
-                                      None if temps is None else temps[a:b])
-                self.h_out[:b - a].copy_(dev, non_blocking=False)
-                out[a:b] = self.h_out.numpy()[:b - a]
-            first_eager = d1
-        else:
-            first_eager = d0
+        cu = batch.cu_seqlens
+        feed = batch.feed_src
+        use_graph = bool(self.graphs) and d1 > d0
+        first_eager = d1 if use_graph else d0
+        samp = np.nonzero(batch.samples[first_eager:])[0]
+        # temperatures of the sampled rows: graph rows first, then the eager rows, one copy
+        temps_dev_g = temps_dev_e = None
+        if temps is not None and np.any(temps > 0):
+            ht = self.h_temps[slot].numpy()
+            ng = d1 - d0 if use_graph else 0
+            if ng:
+                ht[:ng] = temps[d0:d1]
+            ht[ng:ng + len(samp)] = temps[first_eager + samp]
+            self.d_temps[:ng + len(samp)].copy_(self.h_temps[slot][:ng + len(samp)], non_blocking=True)
+            temps_dev_g = self.d_temps[:ng] if ng else None
+            temps_dev_e = self.d_temps[ng:ng + len(samp)]
+        out = self.d_sampled[slot]
+        if use_graph:
+            t0 = cu[d0:d1]
+            n = d1 - d0
+            B = next(b for b in sorted(self.graphs) if b >= n)
+            need_feed = self._stage_graph_rows(batch.tokens[t0], batch.positions[t0], batch.block_tables[d0:d1], B,
+                                               None if feed is None else feed[t0], slot)
+            if need_feed:
+                fused.feed_tokens(self.g_tok[:n], self.g_feed[:n], self._prev_sampled())
+            self.graphs[B].replay()
+            self._sample(self.g_hidden[:n], out[d0:d1], temps_dev_g)
         if first_eager < S:
             a = first_eager
-            cu = batch.cu_seqlens
             t_lo, t_hi = cu[a], cu[S]
             rows_cu = cu[a:] - t_lo
-            samp = np.nonzero(batch.samples[a:])[0]
             last_tok = rows_cu[samp + 1] - 1
             tables = batch.block_tables[a:]
             W = min(tables.shape[1], self.table_width)
-            dev = self._run_eager(batch.tokens[t_lo:t_hi], batch.positions[t_lo:t_hi], rows_cu, tables[:, :W],
-                                  last_tok, None if temps is None else temps[a + samp])
-            pending.append((a + samp, dev))
-        for idx, dev in pending:
-            n = len(idx)
-            if n:
-                self.h_out[:n].copy_(dev, non_blocking=False)
-                out[idx] = self.h_out.numpy()[:n]
-        return out
+            self._run_eager(batch.tokens[t_lo:t_hi], batch.positions[t_lo:t_hi], rows_cu, tables[:, :W], last_tok,
+                            temps_dev_e, None if feed is None else feed[t_lo:t_hi], slot, a + samp, out)
+        self.h_sampled[slot][:S].copy_(out[:S], non_blocking=True)
+        self.events[slot].record()
+        self.last_slot, self.slot = slot, slot ^ 1
+        return (slot, S, batch.samples.copy())
+
+    def collect(self, handle) -> np.ndarray:
+        """Wait for a launched step and return its sampled token per row (-1 where none)."""
+        slot, S, samples = handle
+        self.events[slot].synchronize()
+        vals = self.h_sampled[slot][:S].numpy().copy()
+        vals[~samples] = -1
+        return vals
+
+    def run(self, batch, temps: np.ndarray | None = None) -> np.ndarray:
+        """launch + collect (a synchronous step)."""
+        return self.collect(self.launch(batch, temps))

@@ -25,7 +25,8 @@ enum {
     CVE_ERR_INVALID_ARG = -1,
     CVE_ERR_TOO_LONG = -2,        /* a request needs more KV blocks than the cache has */
     CVE_ERR_STATE = -3,           /* call out of order (e.g. postprocess without a batch) */
-    CVE_ERR_EMPTY = -4            /* requests pending but nothing could be scheduled */
+    CVE_ERR_EMPTY = -4,           /* requests pending but nothing could be scheduled */
+    CVE_ERR_BUSY = -5             /* nothing can be scheduled until the oldest step is post-processed */
 };
 
 /* Step groups, in the order they appear in a batch (model_runner.cpp:178-196 of the reference):
@@ -47,7 +48,10 @@ typedef struct cve_config {
  * ordered by group; group g holds sequences [group_start[g], group_start[g+1]). Row j of the
  * flat batch: tokens/positions [cu_seqlens[j], cu_seqlens[j+1]), kv_lens[j] = cached + new
  * tokens, block table row j (table_width entries, -1 padded), samples[j] = 1 when the step
- * produces the sequence's next token (its last scheduled token is the last of its context). */
+ * produces the sequence's next token (its last scheduled token is the last of its context).
+ * feed_src[t] >= 0 marks a token that the previous step (still unprocessed) is sampling:
+ * tokens[t] is -1 and the runner must copy row feed_src[t] of that step's sampled tokens into it
+ * on the device (kernels/fused_ops.cu:379-397, cvh_feed_tokens). */
 typedef struct cve_batch {
     int64_t num_seqs, num_tokens, table_width;
     int64_t group_start[CVE_NUM_GROUPS + 1];
@@ -58,6 +62,7 @@ typedef struct cve_batch {
     const int64_t* block_tables;    /* [num_seqs][table_width] */
     const int8_t* samples;          /* [num_seqs] */
     const int64_t* seq_ids;         /* [num_seqs] request id of each row */
+    const int64_t* feed_src;        /* [num_tokens] row of the previous step's sampled tokens, or -1 */
 } cve_batch;
 
 typedef struct cve_stats {
@@ -73,15 +78,21 @@ void cve_destroy(void* engine);
 int64_t cve_add_request(void* engine, const int32_t* prompt, int64_t prompt_len, int32_t max_tokens,
                         int32_t ignore_eos);
 
-/* Build the next step (scheduler.cpp:37-103 + on_launched :105-119). CVE_OK with
- * out->num_seqs == 0 when nothing is pending; CVE_ERR_EMPTY if requests wait but none fits. */
+/* Build the next step (scheduler.cpp:37-103 + on_launched :105-119). Up to two steps may be
+ * outstanding (scheduled, not yet post-processed; the reference's launch ring, llm_engine.h:51):
+ * a step built while another is outstanding never preempts and reads that step's samples through
+ * feed_src. CVE_OK with out->num_seqs == 0 when nothing is pending; CVE_ERR_EMPTY if requests wait
+ * but none fits; CVE_ERR_BUSY if nothing can run until the oldest step is post-processed;
+ * CVE_ERR_STATE if two steps are already outstanding. */
 int cve_schedule(void* engine, cve_batch* out);
 
-/* Accept the sampled tokens of the last scheduled step, one per row in batch order (rows with
- * samples[j] == 0 are ignored) (scheduler.cpp:121-154). */
+/* Accept the sampled tokens of the OLDEST outstanding step, one per row in its batch order (rows
+ * with samples[j] == 0 are ignored) (scheduler.cpp:121-154). A sequence that finished in an
+ * older step ignores its row; its blocks are freed once no outstanding step contains it. */
 int cve_postprocess(void* engine, const int64_t* sampled, int64_t num_seqs);
 
-int cve_is_finished(void* engine);        /* 1 when no request is waiting or running */
+int cve_is_finished(void* engine);        /* 1 when no request is waiting or running and no step is outstanding */
+int64_t cve_num_outstanding(void* engine); /* scheduled steps not yet post-processed (0..2) */
 int cve_get_stats(void* engine, cve_stats* out);
 
 /* Finished requests: cve_num_finished() of them, in request-id order; cve_finished_output copies

@@ -6,7 +6,7 @@ hits, preemption) and by invariants over seeded random workloads."""
 import numpy as np
 import pytest
 
-from cppvllm_amd.engine_core import GROUP_CONT, GROUP_DECODE, GROUP_FRESH, EngineCore
+from cppvllm_amd.engine_core import GROUP_CONT, GROUP_DECODE, GROUP_FRESH, EngineBusy, EngineCore
 
 
 def run_to_end(core, token_fn=lambda sid, step: 7, max_steps=100000):
@@ -217,3 +217,124 @@ def test_random_workload_invariants(seed):
         assert len(out[rid]) == m
         assert out[rid] == ctx[rid][len(p):]
     assert core.stats().free_blocks == nblocks
+
+
+# ---- two-deep launch ring (engine/llm_engine.cpp:70-113) -------------------------------------------------
+V = 997
+
+
+def fake_model(b, prev_sampled):
+    """Next token of every sampling row from its context's last token and position; tokens the
+    previous step is sampling (feed_src >= 0) are read from that step's samples, as the device
+    feed does."""
+    toks = b.tokens.copy()
+    feed = b.feed_src
+    if feed is not None and (feed >= 0).any():
+        assert prev_sampled is not None
+        toks[feed >= 0] = prev_sampled[feed[feed >= 0]]
+    assert (toks >= 0).all()
+    out = np.full(b.num_seqs, -1, dtype=np.int64)
+    for j in range(b.num_seqs):
+        if b.samples[j]:
+            t = b.cu_seqlens[j + 1] - 1
+            out[j] = (int(toks[t]) * 31 + int(b.positions[t]) * 7 + 3) % V
+    return out
+
+
+def drive(core, depth):
+    """Run to completion keeping up to `depth` steps outstanding; returns the step count."""
+    ring = []                 # (batch, sampled) of outstanding steps, oldest first
+    steps = 0
+    while not core.is_finished():
+        if len(ring) < depth:
+            try:
+                b = core.schedule()
+            except EngineBusy:
+                b = "busy"
+            if b is not None and b != "busy":
+                prev = ring[-1][1] if ring else None
+                ring.append((b, fake_model(b, prev)))
+                steps += 1
+                assert steps < 20000
+                if len(ring) < depth:
+                    continue
+            elif b is None and not ring:
+                break
+        _, s = ring.pop(0)
+        core.postprocess(s)
+    while ring:
+        core.postprocess(ring.pop(0)[1])
+    return steps
+
+
+def make_core(**kw):
+    return EngineCore(block_size=16, num_blocks=kw.pop("num_blocks", 400), max_num_batched_tokens=256,
+                      max_num_seqs=kw.pop("max_num_seqs", 16), max_chunk_tokens=64, **kw)
+
+
+def workload(core, seed, n=40, eos=False):
+    rng = np.random.default_rng(seed)
+    ids = []
+    for _ in range(n):
+        p = rng.integers(0, V, int(rng.integers(1, 120))).tolist()
+        ids.append(core.add_request(p, max_tokens=int(rng.integers(1, 50)), ignore_eos=not eos))
+    return ids
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("eos", [False, True])
+def test_ring_matches_synchronous_steps(seed, eos):
+    outs = []
+    for depth in (1, 2):
+        core = make_core(eos_token_id=5 if eos else -1)
+        ids = workload(core, seed, eos=eos)
+        drive(core, depth)
+        got = core.take_finished()
+        outs.append([got[i] for i in ids])
+        assert core.stats().free_blocks == 400
+        assert core.outstanding() == 0
+    assert outs[0] == outs[1]
+    if eos:   # some request did stop at the EOS token
+        assert any(o and o[-1] == 5 for o in outs[1])
+
+
+def test_ring_feeds_the_previous_steps_samples():
+    core = make_core()
+    rid = core.add_request([1, 2, 3], max_tokens=4)
+    b0 = core.schedule()                         # prefill, samples token 3's successor
+    assert b0.samples[0] and (b0.feed_src == -1).all()
+    b1 = core.schedule()                         # decode of the token b0 is still sampling
+    assert list(b1.tokens) == [-1] and list(b1.feed_src) == [0] and list(b1.positions) == [3]
+    with pytest.raises(RuntimeError):
+        core.schedule()                          # two steps outstanding
+    assert core.outstanding() == 2
+    core.postprocess([40])
+    b2 = core.schedule()
+    assert list(b2.feed_src) == [0] and list(b2.positions) == [4]
+    core.postprocess([41])
+    core.postprocess([42])
+    b3 = core.schedule()                         # synchronous again: the token is known
+    assert list(b3.tokens) == [42] and list(b3.feed_src) == [-1]
+    core.postprocess([43])
+    assert core.is_finished() and core.take_finished() == {rid: [40, 41, 42, 43]}
+
+
+def test_ring_does_not_schedule_past_max_tokens():
+    core = make_core()
+    rid = core.add_request([9, 9], max_tokens=1)
+    core.schedule()                              # its only token is being sampled
+    with pytest.raises(EngineBusy):
+        core.schedule()                          # nothing else to run until that step retires
+    core.postprocess([77])
+    assert core.is_finished() and core.take_finished() == {rid: [77]}
+
+
+def test_ring_defers_preemption_until_drained():
+    core = EngineCore(block_size=16, num_blocks=6, max_num_batched_tokens=256, max_num_seqs=4)
+    a = core.add_request(list(range(40)), max_tokens=40)     # 3 blocks now, 5 at the end
+    b = core.add_request(list(range(100, 130)), max_tokens=40)
+    steps = drive(core, 2)
+    out = core.take_finished()
+    assert len(out[a]) == 40 and len(out[b]) == 40
+    assert core.stats().preemptions >= 1 and core.stats().free_blocks == 6
+    assert steps > 0

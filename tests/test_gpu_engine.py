@@ -176,7 +176,21 @@ def test_generate_greedy_with_chunked_prefill_and_graphs():
     st = eng.stats()
     assert st.tokens_sampled == 60 and st.finished == 6
     # the same requests alone, eagerly: the first generated token (prefill logits) agrees
-    eng2 = _engine(enforce_eager=True, max_num_seqs=4, blocks=64)
+    eng2 = _engine(enforce_eager=True, max_num_seqs=4, blocks=64, depth=1)
     first = [eng2.generate([p], SamplingParams(max_tokens=1, ignore_eos=True))[0][0] for p in prompts]
     agree = sum(int(a[0] == b) for a, b in zip(outs, first))
     assert agree >= 5, (outs, first)
+
+
+def test_launch_ring_equals_synchronous_steps():
+    say("engine: two-deep launch ring (device token feedback) vs synchronous steps")
+    g = torch.Generator().manual_seed(24)
+    prompts = [torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (5, 70, 33, 140, 9)]
+    params = [SamplingParams(max_tokens=n, ignore_eos=True) for n in (20, 3, 17, 9, 25)]
+    outs = []
+    for depth in (1, 2):
+        eng = _engine(depth=depth, max_num_seqs=8, blocks=64)
+        outs.append(eng.generate(prompts, params))
+        assert eng.core.outstanding() == 0 and eng.stats().free_blocks == 64
+    assert outs[0] == outs[1]
+    assert [len(o) for o in outs[1]] == [20, 3, 17, 9, 25]
