@@ -303,6 +303,8 @@ def main():
                     help="3: 256 seqs, ctx U(100,1024)+U(0,1024) (headline); 4: 64 seqs, ctx log-U(4k,32k); "
                          "2: the fused pre-attention ops over 4096 packed tokens")
     ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
+    ap.add_argument("--no-shared-reuse", action="store_true",
+                    help="config 4b without telling the plan which blocks are shared (all reads non-temporal)")
     ap.add_argument("--e2e", action="store_true", help="config 5: end-to-end generation tok/s through the engine")
     ap.add_argument("--e2e-requests", type=int, default=256)
     ap.add_argument("--prefill", action="store_true", help="time the MFMA multi-query (prefill) kernel alone")
@@ -362,7 +364,11 @@ def main():
     # the op = decode kernel (split phase) + merge of cut rows (merge phase); by default a plan of
     # the step's layout is built once per step and read by every layer's decode launch
     planned = not args.unplanned
-    split_fn = lib.cvh_paged_attention_fp8_planned_split_phase if planned else lib.cvh_paged_attention_fp8_split_phase
+    split_fn = lib.cvh_paged_attention_fp8_split_phase
+    if planned:
+        split_fn = lib.cvh_paged_attention_fp8_planned_split_phase
+    if planned and args.shared_prefix and not args.no_shared_reuse:
+        split_fn = lib.cvh_paged_attention_fp8_planned_shared_split_phase
     merge_fn = lib.cvh_paged_attention_fp8_merge_phase
 
     def launch(fn, lp):
@@ -373,11 +379,18 @@ def main():
         if code:
             raise _lib.CvhError("paged_attention_fp8", code)
 
+    shared = args.shared_prefix and not args.no_shared_reuse and planned
+
     def plan():
         sp = torch.cuda.current_stream(dev).cuda_stream
-        code = lib.cvh_paged_attention_plan(b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(),
-                                            b["token_kv_len"].data_ptr(), T, H, KV, HD, BS, args.partitions,
-                                            ws.data_ptr(), ws_bytes, sp)
+        if shared:        # config 4b: the shared prefix blocks are read cache-resident
+            code = lib.cvh_paged_attention_plan_shared(b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(),
+                                                       b["token_kv_len"].data_ptr(), b["shared_blocks"].data_ptr(), T,
+                                                       H, KV, HD, BS, args.partitions, ws.data_ptr(), ws_bytes, sp)
+        else:
+            code = lib.cvh_paged_attention_plan(b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(),
+                                                b["token_kv_len"].data_ptr(), T, H, KV, HD, BS, args.partitions,
+                                                ws.data_ptr(), ws_bytes, sp)
         if code:
             raise _lib.CvhError("paged_attention_plan", code)
 
@@ -455,7 +468,8 @@ def main():
             if args.partitions == 0 else args.partitions,
             "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "launch": "eager" if args.eager else "hip_graph",
-            "plan": "once per step (cvh_paged_attention_plan), read by all layers" if planned else "none",
+            "plan": ("once per step (%s), read by all layers" % ("cvh_paged_attention_plan_shared" if shared else
+                                                                 "cvh_paged_attention_plan")) if planned else "none",
             "op_us_per_layer": round(total_ms * 1e3 / (args.steps * len(layer_ptrs)), 2),
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

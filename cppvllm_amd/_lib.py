@@ -41,6 +41,11 @@ SIGNATURES = {
     "cvh_paged_attention_fp8_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
                                               f64, vp]),
     "cvh_paged_attention_plan": (i32, [vp, i64, vp, vp, i64, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "cvh_paged_attention_plan_shared": (i32, [vp, i64, vp, vp, vp, i64, i32, i32, i32, i32, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_planned_shared": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32,
+                                                     i32, f64, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_planned_shared_split_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32,
+                                                                 i32, i32, i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
                                               f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned_split_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32,

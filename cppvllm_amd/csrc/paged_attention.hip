@@ -37,6 +37,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "cvh_device.h"
 
@@ -66,13 +67,24 @@ typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
 }
-template <typename VT> __device__ __forceinline__ VT buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
-template <> __device__ __forceinline__ uint4 buf_load<uint4>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+// Blocks that several sequences share (prefix-cache hits) are read with the default policy
+// instead, so the first reader leaves them in L2 / the last-level cache for the others.
+constexpr int kTemporal = 0;
+template <typename VT, int POL = kNonTemporal> __device__ __forceinline__ VT buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
+template <> __device__ __forceinline__ uint4 buf_load<uint4, kNonTemporal>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNonTemporal);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-template <> __device__ __forceinline__ uint2 buf_load<uint2>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+template <> __device__ __forceinline__ uint2 buf_load<uint2, kNonTemporal>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNonTemporal);
+    return make_uint2(v[0], v[1]);
+}
+template <> __device__ __forceinline__ uint4 buf_load<uint4, kTemporal>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kTemporal);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+template <> __device__ __forceinline__ uint2 buf_load<uint2, kTemporal>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kTemporal);
     return make_uint2(v[0], v[1]);
 }
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -173,6 +185,8 @@ struct Params {
     uint16_t* out;
     const PlanRec* plan;     // [G] (planned launches)
     int2* plan_tok;          // [T] (kv_len, block-table row) per token, written by the plan kernel
+    int* shared_tok;         // [T] keys of token t in blocks shared with another sequence (plan kernel)
+    const int32_t* shared_blocks;   // [table rows] leading shared blocks per row (plan input), or null
     float* part_acc;         // [G][2][WPG][REP][HD]
     float* part_ml;          // [G][2][WPG][REP][2]
     int* prefix_out;         // [rows + 1] row tile prefix, written by workgroup 0 for the merge
@@ -282,10 +296,11 @@ template <typename F> __device__ __forceinline__ int first_row(F pfx, int rows, 
 // descriptors, and its table lookups stay inside block-table row 0).
 struct Piece {
     int row, t, g, kv_len, lt, le;
+    int shared_keys;   // keys [0, shared_keys) sit in blocks shared with other sequences
     int64_t seq;   // block-table row of token t
 };
 
-template <int HD, int REP, int SM, bool ONE_BLOCK, bool PLANNED>
+template <int HD, int REP, int SM, bool ONE_BLOCK, bool PLANNED, bool SHARED = false>
 __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     using V = KvVec<HD>;
     using VT = typename V::T;
@@ -335,7 +350,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     };
     // Keys past kv_len (a row's last tile) are clamped to key kv_len-1: a valid, finite row whose
     // score is masked. live = false (no work left): zero-size descriptors, no memory traffic.
-    auto load_tile = [&](const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
+    auto load_tile_pol = [&](auto pol, const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
+        constexpr int POL = decltype(pol)::value;
         const int p0 = tile * kTileKeys;
         const uint32_t lv = static_cast<uint32_t>(live);             // arithmetic, not a branch
         const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
@@ -346,8 +362,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             const int pos = min(p0 + 8 * s + grp, pc.kv_len - 1);
             const uint32_t in_blk = static_cast<uint32_t>(pos & bs_mask);
             const uint32_t off = in_blk * row_bytes + lane_col;
-            tl.k[s] = buf_load<VT>(make_rsrc(p.k_cache + ph * blk_bytes, kv_rec), off);
-            tl.v[s] = buf_load<VT>(make_rsrc(p.v_cache + ph * blk_bytes, kv_rec), off);
+            tl.k[s] = buf_load<VT, POL>(make_rsrc(p.k_cache + ph * blk_bytes, kv_rec), off);
+            tl.v[s] = buf_load<VT, POL>(make_rsrc(p.v_cache + ph * blk_bytes, kv_rec), off);
             if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
                 const int64_t sbase = (ph * p.n_kv + pc.g) << log2_bs;
                 tl.ks[s] = buf_load_f32(make_rsrc(p.k_scale + sbase, s_rec), in_blk * 4u);
@@ -357,6 +373,14 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 tl.vs[s] = 1.f;
             }
         }
+    };
+
+    // wave-uniform choice of the cache policy: shared-prefix tiles stay cacheable
+    auto load_tile = [&](const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
+        if (SHARED && tile * kTileKeys < pc.shared_keys)
+            load_tile_pol(std::integral_constant<int, kTemporal>{}, pc, tile, tl, ph2, live);
+        else
+            load_tile_pol(std::integral_constant<int, kNonTemporal>{}, pc, tile, tl, ph2, live);
     };
 
     Tile A, B, C;
@@ -404,6 +428,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             pc.le = ld_uniform(&rp->le, 0);
             pc.kv_len = live ? ld_uniform(&rp->kv_len, 0) : 1;
             pc.seq = ld_uniform(&rp->seq, 0);
+            pc.shared_keys = (SHARED && live) ? ld_uniform(p.shared_tok, pc.t) : 0;
             const bool b_ok = live && ld_uniform(&rp->b_ok, 0) != 0;
             load_tile(pc, plan_lt, A, {ld_uniform(&rp->a_lo, 0), ld_uniform(&rp->a_hi, 0)}, live);
             load_tile(pc, plan_lt + 1, B, {ld_uniform(&rp->b_lo, 0), ld_uniform(&rp->b_hi, 0)}, b_ok);
@@ -460,6 +485,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             pc.g = (r % hg_count) * wpg + wi;
             const int2 tm = tok[pc.t];
             pc.kv_len = uniform(tm.x);
+            pc.shared_keys = SHARED ? ld_uniform(p.shared_tok, pc.t) : 0;
             pc.lt = static_cast<int>(max(u0, pr0) - pr0);
             pc.le = static_cast<int>(min(u1, pr1) - pr0);
             pc.seq = uniform(tm.y);
@@ -473,6 +499,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         none.lt = 0;
         none.le = 1;
         none.seq = 0;
+        none.shared_keys = 0;
         return none;
     };
 
@@ -778,7 +805,15 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* pla
     int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows));
     build_row_prefix(p, rows, hg_count, prefix, tok);
     for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
-    for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) p.plan_tok[t] = tok[t];
+    for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) {
+        p.plan_tok[t] = tok[t];
+        int sh = 0;
+        if (p.shared_blocks != nullptr) {
+            const int64_t nb = p.shared_blocks[tok[t].y];
+            sh = static_cast<int>(min(static_cast<int64_t>(tok[t].x), max(nb, int64_t{0}) << p.log2_bs));
+        }
+        p.shared_tok[t] = sh;
+    }
     const int64_t U = prefix[rows];
     const int log2_bs = p.log2_bs;
     auto pf = [&](int i) { return prefix[i]; };
@@ -841,9 +876,9 @@ int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
 }
 
 // Workspace: prefix int32 [rows + 1] | part_acc float [G][2][WPG][REP][HD] | part_ml float2 [...]
-// | plan: token metadata int2 [T], workgroup records PlanRec [G]
+// | plan: token metadata int2 [T], shared-prefix keys int32 [T], workgroup records PlanRec [G]
 struct Workspace {
-    size_t prefix_off, acc_off, ml_off, tok_off, plan_off, total;
+    size_t prefix_off, acc_off, ml_off, tok_off, shared_off, plan_off, total;
 };
 size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
 Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
@@ -855,13 +890,15 @@ Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
     w.acc_off = align256(static_cast<size_t>(rows + 1) * sizeof(int));
     w.ml_off = w.acc_off + align256(static_cast<size_t>(slots) * HD * sizeof(float));
     w.tok_off = w.ml_off + align256(static_cast<size_t>(slots) * 2 * sizeof(float));
-    w.plan_off = w.tok_off + align256(static_cast<size_t>(T) * sizeof(int2));
+    w.shared_off = w.tok_off + align256(static_cast<size_t>(T) * sizeof(int2));
+    w.plan_off = w.shared_off + align256(static_cast<size_t>(T) * sizeof(int));
     w.total = w.plan_off + align256(static_cast<size_t>(G) * sizeof(PlanRec));
     return w;
 }
 
 // kPhasePlanned: the decode phase reads the plan kPhasePlan left in the workspace
-enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3, kPhasePlanned = 4, kPhasePlan = 8 };
+// kPhaseShared (with kPhasePlanned): also read the plan's shared-prefix keys (cache-resident loads)
+enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3, kPhasePlanned = 4, kPhasePlan = 8, kPhaseShared = 16 };
 
 template <typename K>
 void launch_with_lds(K kernel, int G, int threads, size_t lds, hipStream_t s, const Params& p) {
@@ -871,24 +908,27 @@ void launch_with_lds(K kernel, int G, int threads, size_t lds, hipStream_t s, co
     kernel<<<dim3(G), threads, lds, s>>>(p);
 }
 
-template <int HD, int REP, int SM, bool PLANNED>
+// planned: 0 = derive the layout, 1 = read the plan, 2 = read the plan and its shared-prefix keys
+template <int HD, int REP, int SM, bool PLANNED, bool SHARED>
 void launch_decode_p(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
     if (one_block)
-        launch_with_lds(paged_decode_kernel<HD, REP, SM, true, PLANNED>, G, threads, lds, s, p);
+        launch_with_lds(paged_decode_kernel<HD, REP, SM, true, PLANNED, SHARED>, G, threads, lds, s, p);
     else
-        launch_with_lds(paged_decode_kernel<HD, REP, SM, false, PLANNED>, G, threads, lds, s, p);
+        launch_with_lds(paged_decode_kernel<HD, REP, SM, false, PLANNED, SHARED>, G, threads, lds, s, p);
 }
 template <int HD, int REP, int SM>
-void launch_decode(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block, bool planned) {
-    if (planned)
-        launch_decode_p<HD, REP, SM, true>(G, threads, lds, s, p, one_block);
+void launch_decode(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block, int planned) {
+    if (planned == 2)
+        launch_decode_p<HD, REP, SM, true, true>(G, threads, lds, s, p, one_block);
+    else if (planned == 1)
+        launch_decode_p<HD, REP, SM, true, false>(G, threads, lds, s, p, one_block);
     else
-        launch_decode_p<HD, REP, SM, false>(G, threads, lds, s, p, one_block);
+        launch_decode_p<HD, REP, SM, false, false>(G, threads, lds, s, p, one_block);
 }
 
 template <int HD, int SM>
 bool launch_decode_rep(int rep, int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block,
-                       bool planned) {
+                       int planned) {
     switch (rep) {
         case 1: launch_decode<HD, 1, SM>(G, threads, lds, s, p, one_block, planned); return true;
         case 2: launch_decode<HD, 2, SM>(G, threads, lds, s, p, one_block, planned); return true;
@@ -902,7 +942,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
                     const float* v_scale, const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
                     const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
                     int block_size, int scale_mode, double scale, int partitions, void* workspace,
-                    size_t workspace_bytes, cvh_stream_t stream, int phase) {
+                    size_t workspace_bytes, cvh_stream_t stream, int phase, const int32_t* shared_blocks = nullptr) {
     if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0 || partitions < 0)
         return CVH_ERR_INVALID_ARG;
     if (num_tokens == 0) return CVH_OK;
@@ -934,6 +974,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     PlanRec* plan = reinterpret_cast<PlanRec*>(wsb + wl.plan_off);
     p.plan = plan;
     p.plan_tok = reinterpret_cast<int2*>(wsb + wl.tok_off);
+    p.shared_tok = reinterpret_cast<int*>(wsb + wl.shared_off);
+    p.shared_blocks = shared_blocks;
     p.part_acc = reinterpret_cast<float*>(wsb + wl.acc_off);
     p.part_ml = reinterpret_cast<float*>(wsb + wl.ml_off);
     p.q = static_cast<const uint16_t*>(q);
@@ -965,7 +1007,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
     if (phase & kPhaseDecode) {
-        const bool planned = (phase & kPhasePlanned) != 0;
+        const int planned = (phase & kPhasePlanned) ? ((phase & kPhaseShared) ? 2 : 1) : 0;
         const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens)) +
                            static_cast<size_t>(p.qrows) * wpg * rep * head_dim * 2;
         const bool one_block = (1 << lg) >= kTileKeys;
@@ -1049,6 +1091,12 @@ extern "C" int cvh_paged_attention_fp8_planned(CVH_PA_PARAMS) {
 extern "C" int cvh_paged_attention_fp8_planned_split_phase(CVH_PA_PARAMS) {
     return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseDecode | cvh::kPhasePlanned);
 }
+extern "C" int cvh_paged_attention_fp8_planned_shared(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseBoth | cvh::kPhasePlanned | cvh::kPhaseShared);
+}
+extern "C" int cvh_paged_attention_fp8_planned_shared_split_phase(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseDecode | cvh::kPhasePlanned | cvh::kPhaseShared);
+}
 extern "C" int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
                                         const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads,
                                         int head_dim, int block_size, int partitions, void* workspace,
@@ -1057,6 +1105,18 @@ extern "C" int cvh_paged_attention_plan(const int64_t* block_tables, int64_t tab
                                 token_seq, token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size,
                                 CVH_SCALE_PER_TOKEN_HEAD, 1.0, partitions, workspace, workspace_bytes, stream,
                                 cvh::kPhasePlan);
+}
+
+extern "C" int cvh_paged_attention_plan_shared(const int64_t* block_tables, int64_t table_width,
+                                               const int64_t* token_seq, const int64_t* token_kv_len,
+                                               const int32_t* shared_blocks, int64_t num_tokens, int n_heads,
+                                               int n_kv_heads, int head_dim, int block_size, int partitions,
+                                               void* workspace, size_t workspace_bytes, cvh_stream_t stream) {
+    if (shared_blocks == nullptr) return CVH_ERR_INVALID_ARG;
+    return cvh::paged_attention(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, block_tables, table_width,
+                                token_seq, token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size,
+                                CVH_SCALE_PER_TOKEN_HEAD, 1.0, partitions, workspace, workspace_bytes, stream,
+                                cvh::kPhasePlan, shared_blocks);
 }
 
 extern "C" int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,

@@ -51,29 +51,39 @@ def paged_attention_workspace(num_tokens: int, n_heads: int, n_kv_heads: int, he
 
 
 def paged_attention_plan(block_tables, token_seq, token_kv_len, n_heads: int, n_kv_heads: int, head_dim: int,
-                         block_size: int, workspace: torch.Tensor, partitions: int = 0) -> None:
+                         block_size: int, workspace: torch.Tensor, partitions: int = 0,
+                         shared_blocks: torch.Tensor | None = None) -> None:
     """Build the per-step plan that ``paged_attention_fp8(..., planned=True)`` reads from `workspace`
-    (once per batch layout, before the layers of a step)."""
+    (once per batch layout, before the layers of a step). shared_blocks (int32, one per table row):
+    leading blocks each row shares with other rows (prefix-cache hits), read cache-resident."""
     T = token_seq.size(0)
     if T == 0:
         return
-    _require_cuda(block_tables, token_seq, token_kv_len, workspace)
-    code = _lib.lib().cvh_paged_attention_plan(
-        block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(), token_kv_len.data_ptr(), T,
-        int(n_heads), int(n_kv_heads), int(head_dim), int(block_size), int(partitions), workspace.data_ptr(),
-        workspace.numel() * workspace.element_size(), _stream(token_seq))
+    _require_cuda(block_tables, token_seq, token_kv_len, workspace, shared_blocks)
+    L = _lib.lib()
+    common = (T, int(n_heads), int(n_kv_heads), int(head_dim), int(block_size), int(partitions), workspace.data_ptr(),
+              workspace.numel() * workspace.element_size(), _stream(token_seq))
+    if shared_blocks is None:
+        code = L.cvh_paged_attention_plan(block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(),
+                                          token_kv_len.data_ptr(), *common)
+    else:
+        if shared_blocks.dtype != torch.int32:
+            raise ValueError("shared_blocks must be int32")
+        code = L.cvh_paged_attention_plan_shared(block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(),
+                                                 token_kv_len.data_ptr(), shared_blocks.data_ptr(), *common)
     check("paged_attention_plan", code)
 
 
 def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len,
                         scale: float, *, workspace: torch.Tensor | None = None, partitions: int = 0,
-                        planned: bool = False) -> None:
+                        planned: bool = False, shared: bool = False) -> None:
     """FP8 paged attention over a ragged batch of query tokens (kernels/paged_attention.cu:459-473).
 
     out, q: bf16 [T, H, HD]; k_cache, v_cache: uint8 [NB, BS, KV, HD]; k_scale, v_scale: float32
     [NB, BS, KV] (memory order [NB][KV][BS]) or one element each (per-tensor); block_tables int64
     [S, W]; token_seq, token_kv_len int64 [T]. planned=True reads the plan that
-    ``paged_attention_plan`` left in `workspace` for the same layout.
+    ``paged_attention_plan`` left in `workspace` for the same layout; shared=True also reads the
+    shared-prefix keys of a plan built with shared_blocks (cache-resident loads of those blocks).
     """
     T = q.size(0)
     if T == 0:
@@ -86,7 +96,9 @@ def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables
         if planned:
             raise ValueError("planned=True needs the workspace the plan was built in")
         workspace = paged_attention_workspace(T, H, KV, HD, W, BS, partitions, q.device)
-    fn = _lib.lib().cvh_paged_attention_fp8_planned if planned else _lib.lib().cvh_paged_attention_fp8_ex
+    L = _lib.lib()
+    fn = (L.cvh_paged_attention_fp8_planned_shared if shared else L.cvh_paged_attention_fp8_planned) if planned \
+        else L.cvh_paged_attention_fp8_ex
     code = fn(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
         v_scale.data_ptr(), block_tables.data_ptr(), W, token_seq.data_ptr(), token_kv_len.data_ptr(), T, H, KV,

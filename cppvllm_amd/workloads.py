@@ -123,6 +123,9 @@ def decode_batch(ctx_lens: list[int], bs: int, seed: int, device="cpu", per_tens
         "token_kv_len": torch.tensor(ctx_lens, dtype=torch.int64).to(device),
         "block_size": bs, "n_heads": H, "n_kv_heads": KV, "head_dim": HD,
         "scale": 1.0 / math.sqrt(HD), "num_blocks": nb,
+        # leading blocks of each table row that other rows also reference (prefix-cache hits)
+        "shared_blocks": torch.tensor([min(shared_prefix_blocks, n) if (shared_prefix_blocks and i % 2 == 0) else 0
+                                       for i, n in enumerate(nblk)], dtype=torch.int32).to(device),
     }
 
 

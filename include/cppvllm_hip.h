@@ -136,6 +136,32 @@ int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, c
                              const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads,
                              int head_dim, int block_size, int partitions, void* workspace, size_t workspace_bytes,
                              cvh_stream_t stream);
+/* cvh_paged_attention_plan with prefix-cache sharing: shared_blocks[r] (int32, one per
+ * block-table row) is how many leading blocks of row r are also referenced by other rows. The
+ * _planned_shared launches (same arguments as _planned) read those blocks' K/V with the default
+ * cache policy (the rest non-temporal), so the first sequence to read a shared block leaves it in
+ * L2 / the last-level cache for the others. Results are bitwise those of the plain plan and
+ * launches; the plain _planned launches ignore the sharing (no per-tile test in their loop).
+ * (Serves SURVEY §8(f) prefix-shared reuse; no reference counterpart: the reference re-reads
+ *  shared blocks per sequence, engine/block_manager.cpp:80-116 hands out the shared ids.) */
+int cvh_paged_attention_plan_shared(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
+                                    const int64_t* token_kv_len, const int32_t* shared_blocks, int64_t num_tokens,
+                                    int n_heads, int n_kv_heads, int head_dim, int block_size, int partitions,
+                                    void* workspace, size_t workspace_bytes, cvh_stream_t stream);
+int cvh_paged_attention_fp8_planned_shared(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                           const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                           int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                                           int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                           int block_size, int scale_mode, double scale, int partitions,
+                                           void* workspace, size_t workspace_bytes, cvh_stream_t stream);
+int cvh_paged_attention_fp8_planned_shared_split_phase(void* out, const void* q, const uint8_t* k_cache,
+                                                       const uint8_t* v_cache, const float* k_scale,
+                                                       const float* v_scale, const int64_t* block_tables,
+                                                       int64_t table_width, const int64_t* token_seq,
+                                                       const int64_t* token_kv_len, int64_t num_tokens, int n_heads,
+                                                       int n_kv_heads, int head_dim, int block_size, int scale_mode,
+                                                       double scale, int partitions, void* workspace,
+                                                       size_t workspace_bytes, cvh_stream_t stream);
 int cvh_paged_attention_fp8_planned(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
                                     const float* k_scale, const float* v_scale, const int64_t* block_tables,
                                     int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,

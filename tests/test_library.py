@@ -70,8 +70,9 @@ def test_partition_policy_and_workspace_sizes():
     assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 256
     rows, slots = 256, 256 * 2 * 16     # [G][2][WPG*REP] partial slots
     r256 = lambda v: (v + 255) // 256 * 256
-    # plan: int2 token metadata [T] + 64-byte workgroup records [G]
-    want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4) + r256(256 * 8) + r256(256 * 64)
+    # plan: int2 token metadata [T] + int32 shared-prefix keys [T] + 64-byte workgroup records [G]
+    want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4) + r256(256 * 8) + r256(256 * 4) + \
+        r256(256 * 64)
     assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == want
     # small batches: never less than two tiles per partition
     assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
