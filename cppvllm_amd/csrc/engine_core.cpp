@@ -381,6 +381,7 @@ private:
         cu_.assign(S + 1, 0);
         kv_.assign(S, 0);
         tables_.assign(S * W, -1);
+        shared_.assign(S, 0);
         samples_.assign(S, 0);
         ids_.assign(S, 0);
         int64_t t = 0;
@@ -397,6 +398,10 @@ private:
             cu_[j + 1] = t;
             kv_[j] = kv;
             for (int64_t b = 0; b < ceil_div(kv, cfg_.block_size); ++b) tables_[j * W + b] = s->table[b];
+            // leading blocks another live sequence also references (prefix-cache hits)
+            int32_t sh = 0;
+            while (sh < static_cast<int32_t>(s->table.size()) && bm_.ref_count(s->table[sh]) > 1) ++sh;
+            shared_[j] = sh;
             ids_[j] = s->id;
             const bool samples = kv == s->size();
             samples_[j] = samples ? 1 : 0;
@@ -420,6 +425,7 @@ private:
         out->samples = samples_.data();
         out->seq_ids = ids_.data();
         out->feed_src = feed_.data();
+        out->shared_blocks = shared_.data();
     }
     void finish(Seq* s) {
         Output o;
@@ -445,6 +451,7 @@ private:
     cve_stats stats_{};
     std::vector<int64_t> tokens_, feed_, positions_, cu_, kv_, tables_, ids_;
     std::vector<int8_t> samples_;
+    std::vector<int32_t> shared_;
 };
 
 Engine* E(void* p) { return static_cast<Engine*>(p); }

@@ -32,7 +32,7 @@ class _Batch(C.Structure):
                 ("positions", C.POINTER(C.c_int64)), ("cu_seqlens", C.POINTER(C.c_int64)),
                 ("kv_lens", C.POINTER(C.c_int64)), ("block_tables", C.POINTER(C.c_int64)),
                 ("samples", C.POINTER(C.c_int8)), ("seq_ids", C.POINTER(C.c_int64)),
-                ("feed_src", C.POINTER(C.c_int64))]
+                ("feed_src", C.POINTER(C.c_int64)), ("shared_blocks", C.POINTER(C.c_int32))]
 
 
 class Stats(C.Structure):
@@ -89,6 +89,7 @@ class Batch:
     seq_ids: np.ndarray         # int64 [S]
     group_start: tuple
     feed_src: np.ndarray = None  # int64 [T]: row of the previous step's samples feeding a token, or -1
+    shared_blocks: np.ndarray = None  # int32 [S]: leading blocks other live sequences also reference
 
     @property
     def num_seqs(self) -> int:
@@ -145,7 +146,8 @@ class EngineCore:
                      cu_seqlens=_arr(b.cu_seqlens, S + 1, np.int64), kv_lens=_arr(b.kv_lens, S, np.int64),
                      block_tables=_arr(b.block_tables, S * W, np.int64).reshape(S, W),
                      samples=_arr(b.samples, S, np.int8).astype(bool), seq_ids=_arr(b.seq_ids, S, np.int64),
-                     group_start=tuple(int(x) for x in b.group_start), feed_src=_arr(b.feed_src, T, np.int64))
+                     group_start=tuple(int(x) for x in b.group_start), feed_src=_arr(b.feed_src, T, np.int64),
+                     shared_blocks=_arr(b.shared_blocks, S, np.int32))
 
     def postprocess(self, sampled) -> None:
         s = np.ascontiguousarray(sampled, dtype=np.int64)

@@ -92,7 +92,8 @@ class Qwen3:
         self.cos, self.sin = cos.to(device), sin.to(device)
         self.scale = 1.0 / math.sqrt(HD)
 
-    def forward(self, cache: KVCache, tokens, positions, cu_seqlens, block_tables, workspace, planned: bool):
+    def forward(self, cache: KVCache, tokens, positions, cu_seqlens, block_tables, workspace, planned: bool,
+                shared_blocks=None):
         """Backbone over T ragged tokens; returns the final-normed hidden rows x [T, D]
         (the last layer's add_rms_norm applies the final norm: resid + mlp, then RMSNorm, as
         h.add_(mlp) + rms_norm(h, final_norm) at model_architecture.cpp:188,224)."""
@@ -105,8 +106,10 @@ class Qwen3:
         ops.embedding(h, self.embed, tokens)
         x = torch.empty_like(h)
         fused.rms_norm(x, h, self.attn_norm[0], eps)
-        if planned:
-            ops.paged_attention_plan(block_tables, seq, kvl, H, KV, HD, cache.block_size, workspace)
+        shared = planned and shared_blocks is not None
+        if planned:   # shared_blocks: per-row leading blocks shared with other rows, read cache-resident
+            ops.paged_attention_plan(block_tables, seq, kvl, H, KV, HD, cache.block_size, workspace,
+                                     shared_blocks=shared_blocks if shared else None)
         q = torch.empty((T, H, HD), dtype=bf16, device=dev)
         att = torch.empty_like(q)
         act = torch.empty((T, I), dtype=bf16, device=dev)
@@ -123,7 +126,7 @@ class Qwen3:
                 ops.paged_attention_fp8_prefill(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale)
             else:
                 ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
-                                        workspace=workspace, planned=planned)
+                                        workspace=workspace, planned=planned, shared=shared)
             o = F.linear(att.view(T, H * HD), self.wo[li])
             fused.add_rms_norm(h, o, self.ffn_norm[li], x, eps)
             gu = F.linear(x, self.w_gate_up[li])
@@ -174,13 +177,16 @@ class ModelRunner:
         self.graph_width = Wg = graph_max_blocks or self.table_width
         self.max_graph_batch = Bm = max_num_seqs
         i64 = dict(dtype=torch.int64)
-        # decode-graph inputs, one int64 arena: tok | pos | cu | feed | tables (B x Wg)
-        self.g_off = np.cumsum([0, Bm, Bm, Bm + 1, Bm]).tolist()
+        # decode-graph inputs, one int64 arena: tok | pos | cu | feed | shared blocks (int32 pairs)
+        # | tables (B x Wg)
+        self.g_off = np.cumsum([0, Bm, Bm, Bm + 1, Bm, (Bm + 1) // 2]).tolist()
         self.g_len = self.g_off[-1] + Bm * Wg
         self.d_garena = torch.zeros(self.g_len, device=dev, **i64)
         o = self.g_off
         self.g_tok, self.g_pos = self.d_garena[o[0]:o[1]], self.d_garena[o[1]:o[2]]
-        self.g_cu, self.g_feed, self.g_tab = self.d_garena[o[2]:o[3]], self.d_garena[o[3]:o[4]], self.d_garena[o[4]:]
+        self.g_cu, self.g_feed = self.d_garena[o[2]:o[3]], self.d_garena[o[3]:o[4]]
+        self.g_shared = self.d_garena[o[4]:o[5]].view(torch.int32)
+        self.g_tab = self.d_garena[o[5]:]
         # eager inputs: tok | pos | feed | cu | sampled token rows | their batch rows | tables (S x W)
         self.e_off = np.cumsum([0, Tm, Tm, Tm, Sm + 1, Sm, Sm]).tolist()
         self.e_len = self.e_off[-1] + Sm * Wm
@@ -198,11 +204,13 @@ class ModelRunner:
         self.seed, self.sample_step = seed, 0
         self.ws_eager = ops.paged_attention_workspace(Tm, c.n_heads, c.n_kv_heads, c.head_dim, Wm, BS, 0, dev)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.graphs_shared: dict[int, torch.cuda.CUDAGraph] = {}
+        self.shared_replays = 0
         if not enforce_eager:
             self.capture_graphs()
 
     # ---- decode graphs -------------------------------------------------------------------------
-    def _stage_graph_rows(self, toks, pos, tables, B: int, feed=None, slot: int = 0) -> bool:
+    def _stage_graph_rows(self, toks, pos, tables, B: int, feed=None, slot: int = 0, shared=None) -> bool:
         """Rows [0, S) are the decode rows; [S, B) are idle rows on the scratch block at position 0
         with kv_len 1 (model_runner.cpp:327-357). One host-to-device copy. Returns whether any
         token must be fed from the previous step's samples."""
@@ -215,20 +223,25 @@ class ModelRunner:
         need_feed = feed is not None and bool((feed >= 0).any())
         if need_feed:
             h[o[3]:o[3] + S] = feed
-        tab = h[o[4]:o[4] + B * Wg].reshape(B, Wg)
+        sh = h[o[4]:o[5]].view(np.int32)
+        sh[:B] = 0
+        if shared is not None and S:
+            sh[:S] = shared
+        tab = h[o[5]:o[5] + B * Wg].reshape(B, Wg)
         tab[:] = -1
         if S:
             w = min(tables.shape[1], Wg)
             tab[:S, :w] = tables[:, :w]
         tab[S:B, 0] = self.cache.scratch_block
-        n = o[4] + B * Wg
+        n = o[5] + B * Wg
         self.d_garena[:n].copy_(self.h_garena[slot][:n], non_blocking=True)
         return need_feed
 
-    def _graph_body(self, B: int, ws) -> None:
+    def _graph_body(self, B: int, ws, shared: bool = False) -> None:
         Wg = self.graph_width
         x = self.model.forward(self.cache, self.g_tok[:B], self.g_pos[:B], self.g_cu[:B + 1],
-                               self.g_tab[:B * Wg].view(B, Wg), ws, planned=True)
+                               self.g_tab[:B * Wg].view(B, Wg), ws, planned=True,
+                               shared_blocks=self.g_shared[:B] if shared else None)
         self.g_hidden[:B].copy_(x)
 
     def capture_graphs(self) -> None:
@@ -245,14 +258,17 @@ class ModelRunner:
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            for B in reversed(sizes):
-                for _ in range(2):
-                    self._graph_body(B, self.ws_graph)
-                side.synchronize()
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, pool=pool, stream=side):
-                    self._graph_body(B, self.ws_graph)
-                self.graphs[B] = g
+            # per batch size: the plain decode graph, and a variant whose attention reads the rows'
+            # shared prefix blocks cache-resident (replayed when some decode row shares blocks)
+            for shared, dst in ((False, self.graphs), (True, self.graphs_shared)):
+                for B in reversed(sizes):
+                    for _ in range(2):
+                        self._graph_body(B, self.ws_graph, shared)
+                    side.synchronize()
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, pool=pool, stream=side):
+                        self._graph_body(B, self.ws_graph, shared)
+                    dst[B] = g
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
 
@@ -334,11 +350,15 @@ class ModelRunner:
             t0 = cu[d0:d1]
             n = d1 - d0
             B = next(b for b in sorted(self.graphs) if b >= n)
+            shared = None if batch.shared_blocks is None else batch.shared_blocks[d0:d1]
+            any_shared = shared is not None and bool((shared > 0).any())
             need_feed = self._stage_graph_rows(batch.tokens[t0], batch.positions[t0], batch.block_tables[d0:d1], B,
-                                               None if feed is None else feed[t0], slot)
+                                               None if feed is None else feed[t0], slot,
+                                               shared if any_shared else None)
             if need_feed:
                 fused.feed_tokens(self.g_tok[:n], self.g_feed[:n], self._prev_sampled())
-            self.graphs[B].replay()
+            (self.graphs_shared if any_shared else self.graphs)[B].replay()
+            self.shared_replays += int(any_shared)
             self._sample(self.g_hidden[:n], out[d0:d1], temps_dev_g)
         if first_eager < S:
             a = first_eager

@@ -63,6 +63,8 @@ typedef struct cve_batch {
     const int8_t* samples;          /* [num_seqs] */
     const int64_t* seq_ids;         /* [num_seqs] request id of each row */
     const int64_t* feed_src;        /* [num_tokens] row of the previous step's sampled tokens, or -1 */
+    const int32_t* shared_blocks;   /* [num_seqs] leading table blocks other live sequences also reference
+                                       (cvh_paged_attention_plan_shared) */
 } cve_batch;
 
 typedef struct cve_stats {

@@ -105,6 +105,8 @@ def test_prefix_cache_hits_and_sharing():
     j = list(b.seq_ids).index(b_)
     assert b.kv_lens[j] == 49 and b.cu_seqlens[j + 1] - b.cu_seqlens[j] == 1 and b.positions[b.cu_seqlens[j]] == 48
     assert groups_of(b)[j] == GROUP_DECODE              # one new token on a cached context
+    # both rows report their 3 shared leading blocks (for the attention plan's cache-resident reads)
+    assert list(b.shared_blocks) == [3, 3]
     core.postprocess([7 if s else -1 for s in b.samples])
     run_to_end(core)
     assert core.stats().free_blocks == 32

@@ -194,3 +194,23 @@ def test_launch_ring_equals_synchronous_steps():
         assert eng.core.outstanding() == 0 and eng.stats().free_blocks == 64
     assert outs[0] == outs[1]
     assert [len(o) for o in outs[1]] == [20, 3, 17, 9, 25]
+
+
+def test_prefix_cache_sharing_uses_shared_graphs_with_identical_results():
+    say("engine: prefix-cache hits -> decode graphs with cache-resident shared blocks")
+    g = torch.Generator().manual_seed(25)
+    common = torch.randint(0, SMALL.vocab_size, (64,), generator=g).tolist()       # 4 full 16-token blocks
+    prompts = [common + torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (3, 10, 21, 5)]
+    params = SamplingParams(max_tokens=12, ignore_eos=True)
+    outs = []
+    for use_shared in (True, False):
+        eng = _engine(max_num_seqs=8, blocks=64)
+        if not use_shared:
+            eng.runner.graphs_shared = eng.runner.graphs
+        first = eng.generate(prompts[:1], params)          # fills the prefix cache
+        rest = eng.generate(prompts[1:], params)           # three requests hit the 4 common blocks
+        outs.append(first + rest)
+        assert eng.stats().prefix_hit_tokens >= 3 * 64
+        if use_shared:
+            assert eng.runner.shared_replays > 0
+    assert outs[0] == outs[1]
