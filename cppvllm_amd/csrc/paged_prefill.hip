@@ -166,6 +166,11 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
         const int kmax = __builtin_amdgcn_readfirstlane(kmax_l);
         const int64_t* trow = tables + rseq * W;
         const int row_kvl = (my_seq == rseq) ? my_kvl : 0;
+        // keys this wave's rows need in the run: tiles past it are staged for the other waves only
+        int wk = row_kvl;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) wk = max(wk, __shfl_xor(wk, d, 64));
+        const int wave_kmax = __builtin_amdgcn_readfirstlane(wk);
 
         // cooperative load of tile kb0 into registers (keys >= kmax and negative table entries
         // read as zeros; a negative entry inside a context is invalid input)
@@ -321,7 +326,7 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
         __syncthreads();
         for (int i = 0, kb0 = 0; kb0 < kmax; ++i, kb0 += kTile) {
             const int buf = i & 1;
-            compute(buf, kb0);
+            if (kb0 < wave_kmax) compute(buf, kb0);
             if (kb0 + kTile < kmax) {
                 store_tile(buf ^ 1, rg);
                 load_tile(kb0 + 2 * kTile, rg);
