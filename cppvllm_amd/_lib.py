@@ -63,6 +63,9 @@ SIGNATURES = {
     "cvh_sample_tokens": (i32, [vp, vp, i32, vp, vp, i64, i32, C.c_uint64, C.c_uint64, vp]),
     "cvh_feed_tokens": (i32, [vp, vp, vp, i64, vp]),
     "cvh_embedding": (i32, [vp, vp, vp, i64, i32, i64, vp]),
+    "cvh_gemm_bf16_nt": (i32, [vp, vp, vp, i64, i32, i32, i32, vp]),
+    "cvh_gemm_bf16_nt_config": (i32, [i64, i32, i32]),
+    "cvh_gemm_bf16_nt_configs": (i32, [vp, i32]),
     "cvh_version": (C.c_char_p, []),
 }
 

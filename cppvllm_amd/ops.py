@@ -241,3 +241,24 @@ def fp8_e4m3_quantize(dst, src, inv_scale: float) -> None:
     _require_cuda(dst, src)
     check("fp8_e4m3_quantize", _lib.lib().cvh_fp8_e4m3_quantize(dst.data_ptr(), src.data_ptr(), src.numel(),
                                                                  float(inv_scale), _stream(src)))
+
+
+def gemm_supported(n: int, k: int) -> bool:
+    """Shapes cvh_gemm_bf16_nt takes: N % 16 == 0 and K % 128 == 0."""
+    return n % 16 == 0 and k % 128 == 0
+
+
+def linear(out, x, w, config: int = 0) -> None:
+    """out [M, N] = x [M, K] . w [N, K]^T in bf16 with fp32 accumulation (at::linear of the layer
+    loop, model/model_architecture.cpp:155,178,182,185,224) on the gfx950 MFMA GEMM."""
+    M = x.size(0)
+    if M == 0:
+        return
+    _require_cuda(out, x, w)
+    if not (x.dtype == w.dtype == out.dtype == torch.bfloat16):
+        raise ValueError("linear: bf16 tensors only")
+    N, K = w.shape
+    if x.size(1) != K or tuple(out.shape) != (M, N):
+        raise ValueError(f"linear: shapes x {tuple(x.shape)}, w {tuple(w.shape)}, out {tuple(out.shape)}")
+    check("gemm_bf16_nt", _lib.lib().cvh_gemm_bf16_nt(out.data_ptr(), x.data_ptr(), w.data_ptr(), M, N, K,
+                                                      int(config), _stream(out)))

@@ -3,10 +3,12 @@ HIP-graph-captured decode steps.
 
 Mirrors the reference's runner/model split:
   * ``Qwen3.forward``      — Qwen3::forward_backbone + compute_logits
-                             (model/model_architecture.cpp:130-191,222-236): every non-GEMM op is a
-                             HIP kernel of this package (embedding, norms, QK-norm/RoPE/FP8 cache
-                             write, paged attention, SwiGLU, sampler); the four projections and the
-                             tied lm_head are hipBLASLt GEMMs through torch.
+                             (model/model_architecture.cpp:130-191,222-236): every op is a HIP
+                             kernel of this package (embedding, norms, QK-norm/RoPE/FP8 cache write,
+                             paged attention, SwiGLU, sampler, and the four projections through the
+                             gfx950 GEMM for batches of up to 256 rows, which covers every decode
+                             graph); prompt batches above that and the tied lm_head above 64 rows
+                             use hipBLASLt through torch, which is faster there.
   * ``KVCache``            — ModelRunner::bind_cache layout (engine/model_runner.cpp:104-113):
                              K/V uint8 [L][NB+1][BS][KV][HD], scales f32 [L][NB+1][KV][BS]; block NB
                              is the scratch block that idle graph rows write to (:69,:346).
@@ -28,6 +30,20 @@ import torch.nn.functional as F
 from . import ops
 
 fused = ops.fused
+
+# Row counts up to which cvh_gemm_bf16_nt is faster than hipBLASLt on MI355X (measured over the
+# Qwen3-0.6B projection shapes and the tied lm_head).
+GEMM_MAX_ROWS = 256
+LM_HEAD_MAX_ROWS = 64
+
+
+def _linear(x, w, max_rows: int = GEMM_MAX_ROWS):
+    """x [M, K] . w[N, K]^T in bf16 (at::linear)."""
+    if x.size(0) <= max_rows and ops.gemm_supported(*w.shape):
+        y = torch.empty((x.size(0), w.size(0)), dtype=x.dtype, device=x.device)
+        ops.linear(y, x, w)
+        return y
+    return F.linear(x, w)
 
 
 @dataclass
@@ -119,7 +135,7 @@ class Qwen3:
         multi_query = not planned and T >= 2 * S and ops.prefill_supported(H, KV, HD)
         for li in range(c.n_layers):
             kc, vc, ks, vs = cache.layers[li]
-            qkv = F.linear(x, self.wqkv[li])
+            qkv = _linear(x, self.wqkv[li])
             fused.qk_norm_rope_kv_write_fp8(q, qkv, self.q_norm[li], self.k_norm[li], self.cos, self.sin, positions,
                                             slot, kc, vc, ks, vs, None, None, H, KV, eps)
             if multi_query:
@@ -127,11 +143,11 @@ class Qwen3:
             else:
                 ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
                                         workspace=workspace, planned=planned, shared=shared)
-            o = F.linear(att.view(T, H * HD), self.wo[li])
+            o = _linear(att.view(T, H * HD), self.wo[li])
             fused.add_rms_norm(h, o, self.ffn_norm[li], x, eps)
-            gu = F.linear(x, self.w_gate_up[li])
+            gu = _linear(x, self.w_gate_up[li])
             fused.swiglu(act, gu)
-            m = F.linear(act, self.w_down[li])
+            m = _linear(act, self.w_down[li])
             nxt = self.attn_norm[li + 1] if li + 1 < c.n_layers else self.final_norm
             fused.add_rms_norm(h, m, nxt, x, eps)
         return x
@@ -140,7 +156,7 @@ class Qwen3:
         """Next token of each row (compute_logits + sample_tokens, model_architecture.cpp:222-226,
         model_runner.cpp:262-272): greedy where temps is None or <= 0, else Gumbel-max. Logits
         stay bf16: the reference's float copy of them holds the same values."""
-        logits = F.linear(x_rows, self.embed)
+        logits = _linear(x_rows.contiguous(), self.embed, LM_HEAD_MAX_ROWS)
         fused.sample_tokens(out, logits, None, temps, seed, offset)
 
 

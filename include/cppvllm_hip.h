@@ -275,6 +275,28 @@ int cvh_feed_tokens(int64_t* tokens, const int64_t* src, const int64_t* prev, in
 int cvh_embedding(void* out, const void* table, const int64_t* ids, int64_t num_tokens, int dim, int64_t vocab,
                   cvh_stream_t stream);
 
+/* bf16 GEMM for decode-step projections: y[M][N] = bf16(x[M][K] . w[N][K]^T), fp32 accumulation,
+ * round to nearest even (torch's linear layout: weight rows are output columns).
+ * Replaces: at::linear(x, W) of the layer loop and the lm_head
+ *           (model/model_architecture.cpp:155,178,182,185,224), which the reference runs on cuBLAS.
+ * Requires N % 16 == 0 and K % 128 == 0. config: 0 = automatic (measured best per shape and row
+ * count), otherwise one of the codes cvh_gemm_bf16_nt_configs lists; a code whose tile does not
+ * divide N, or whose K split does not divide K, returns CVH_ERR_UNSUPPORTED. Codes:
+ *   100*xlds + 10*mf + nwn                    streaming kernel (mf row fragments of 16 per wave,
+ *                                             nwn waves across N, K split over 4/nwn waves)
+ *   10000 + 100*nc + 10*mf + nwn              one-shot kernel (exactly nc 128-k chunks per wave)
+ *   100000*st + 20000 + 1000*mf + 100*nf + 10*wm + nwn
+ *                                             tiled kernel (mf x nf fragments per wave, wm x nwn
+ *                                             waves, st LDS stages, 9 = as many as fit)
+ * The sum order depends on the configuration only, so a given configuration is deterministic. */
+int cvh_gemm_bf16_nt(void* y, const void* x, const void* w, int64_t M, int N, int K, int config,
+                     cvh_stream_t stream);
+/* The configuration cvh_gemm_bf16_nt picks for config == 0. */
+int cvh_gemm_bf16_nt_config(int64_t M, int N, int K);
+/* Codes of every compiled configuration: writes min(count, capacity) into codes (may be NULL)
+ * and returns the count. */
+int cvh_gemm_bf16_nt_configs(int* codes, int capacity);
+
 /* Library version string (static storage). */
 const char* cvh_version(void);
 
