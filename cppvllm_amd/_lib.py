@@ -66,6 +66,9 @@ SIGNATURES = {
     "cvh_gemm_bf16_nt": (i32, [vp, vp, vp, i64, i32, i32, i32, vp]),
     "cvh_gemm_bf16_nt_config": (i32, [i64, i32, i32]),
     "cvh_gemm_bf16_nt_configs": (i32, [vp, i32]),
+    "cvh_gemm_bf16_nt_swiglu": (i32, [vp, vp, vp, i64, i32, i32, i32, vp]),
+    "cvh_gemm_bf16_nt_swiglu_config": (i32, [i64, i32, i32]),
+    "cvh_gemm_bf16_nt_swiglu_configs": (i32, [vp, i32]),
     "cvh_version": (C.c_char_p, []),
 }
 

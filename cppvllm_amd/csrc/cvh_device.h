@@ -4,6 +4,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "../../include/cppvllm_hip.h"
@@ -47,6 +48,18 @@ template <> struct Elem<CVH_DTYPE_F32> {
     static __device__ __forceinline__ float load(T v) { return v; }
     static __device__ __forceinline__ T store(float f) { return f; }
 };
+
+// ---- SwiGLU element ---------------------------------------------------------------------------
+// silu(g) * u with the reference's rounding points (kernels/fused_ops.cu:210-219): silu rounded to
+// the storage type, the product left for the caller to round. The exponential is evaluated in
+// double so that the result does not depend on a float exp's last ulp. Shared by the SwiGLU kernel
+// and the gate/up GEMM epilogue, which must agree bit for bit.
+template <int DT>
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const double e = exp(-static_cast<double>(g));
+    const float silu = Elem<DT>::load(Elem<DT>::store(static_cast<float>(static_cast<double>(g) / (1.0 + e))));
+    return silu * u;
+}
 
 // ---- OCP e4m3fn ------------------------------------------------------------------------------
 // Encode with round-to-nearest-even and saturation to +-448 (the __NV_SATFINITE behaviour of the

@@ -381,7 +381,10 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     }
 }
 
-template <int MF, int NF, int WM, int WN, int S>
+// Epilogues of the tiled kernel.
+enum { kEpiStore = 0, kEpiSwiglu = 1 };
+
+template <int MF, int NF, int WM, int WN, int S, int EPI = kEpiStore>
 __global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
                                                          const uint16_t* __restrict__ w, int M, int N, int K) {
     static_assert(WM * WN == 4, "four waves");
@@ -453,16 +456,41 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ 
                                                                         0, 0, 0);
         }
     }
+    if constexpr (EPI == kEpiStore) {
 #pragma unroll
-    for (int f = 0; f < MF; ++f) {
-        const int m = m0 + (wm * MF + f) * 16 + i16;
-        if (m >= M) continue;
+        for (int f = 0; f < MF; ++f) {
+            const int m = m0 + (wm * MF + f) * 16 + i16;
+            if (m >= M) continue;
 #pragma unroll
-        for (int e = 0; e < NF; ++e) {
-            uint2 v;
-            v.x = pack_bf16x2(acc[f][e][0], acc[f][e][1]);
-            v.y = pack_bf16x2(acc[f][e][2], acc[f][e][3]);
-            *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * N + n0 + (wn * NF + e) * 16 + 4 * g) = v;
+            for (int e = 0; e < NF; ++e) {
+                uint2 v;
+                v.x = pack_bf16x2(acc[f][e][0], acc[f][e][1]);
+                v.y = pack_bf16x2(acc[f][e][2], acc[f][e][3]);
+                *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * N + n0 + (wn * NF + e) * 16 + 4 * g) = v;
+            }
+        }
+    } else {
+        // W rows interleaved in blocks of 16 (gate j..j+15, then up j..j+15): fragment pair
+        // (e, e+1) of a lane holds gate and up of the same 4 outputs. y is act [M][N/2]; the
+        // products are rounded to bf16 first, as the reference's gate_up tensor is.
+        static_assert(NF % 2 == 0, "gate/up fragment pairs");
+        const int I = N >> 1;
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int m = m0 + (wm * MF + f) * 16 + i16;
+            if (m >= M) continue;
+#pragma unroll
+            for (int e = 0; e < NF; e += 2) {
+                const int j = ((n0 + (wn * NF + e) * 16) >> 1) + 4 * g;
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    o[r] = silu_mul<CVH_DTYPE_BF16>(round_bf16(acc[f][e][r]), round_bf16(acc[f][e + 1][r]));
+                uint2 v;
+                v.x = pack_bf16x2(o[0], o[1]);
+                v.y = pack_bf16x2(o[2], o[3]);
+                *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * I + j) = v;
+            }
         }
     }
 }
@@ -506,12 +534,27 @@ const GemmCfg kCfgs[] = {
     CVH_GEMM_TILE(1, 1, 4, 1, 3), CVH_GEMM_TILE(1, 1, 2, 2, 3), CVH_GEMM_TILE(1, 1, 1, 4, 3),
     CVH_GEMM_TILE(2, 1, 2, 2, 3), CVH_GEMM_TILE(1, 2, 2, 2, 3), CVH_GEMM_TILE(2, 2, 2, 2, 3),
     CVH_GEMM_TILE(2, 1, 4, 1, 3), CVH_GEMM_TILE(1, 2, 1, 4, 3), CVH_GEMM_TILE(4, 1, 1, 4, 3),
-    CVH_GEMM_TILE(2, 4, 2, 2, 3), CVH_GEMM_TILE(4, 2, 2, 2, 3),
+    CVH_GEMM_TILE(2, 4, 2, 2, 3), CVH_GEMM_TILE(4, 2, 2, 2, 3), CVH_GEMM_TILE(1, 2, 4, 1, 3),
     CVH_GEMM_TILE(1, 1, 2, 2, 0), CVH_GEMM_TILE(1, 1, 4, 1, 0), CVH_GEMM_TILE(2, 1, 2, 2, 0),
 };
 #undef CVH_GEMM_CFG
 #undef CVH_GEMM_ONE
 #undef CVH_GEMM_TILE
+
+// Tiled configurations with the SwiGLU epilogue (an even number of column fragments per wave).
+#define CVH_GEMM_SWIGLU(MF, NF, WM, WN, S) \
+    GemmCfg{MF, WN, 1, 0, gemm_tiled_kernel<MF, NF, WM, WN, S, kEpiSwiglu>, NF, WM, S}
+const GemmCfg kSwigluCfgs[] = {
+    CVH_GEMM_SWIGLU(1, 2, 2, 2, 3), CVH_GEMM_SWIGLU(2, 2, 2, 2, 3), CVH_GEMM_SWIGLU(2, 4, 2, 2, 3),
+    CVH_GEMM_SWIGLU(1, 2, 1, 4, 3), CVH_GEMM_SWIGLU(1, 2, 4, 1, 3), CVH_GEMM_SWIGLU(4, 2, 2, 2, 3),
+};
+#undef CVH_GEMM_SWIGLU
+
+const GemmCfg* find_swiglu_cfg(int code) {
+    for (const GemmCfg& c : kSwigluCfgs)
+        if (c.code() == code) return &c;
+    return nullptr;
+}
 
 const GemmCfg* find_cfg(int code) {
     for (const GemmCfg& c : kCfgs)
@@ -568,6 +611,49 @@ extern "C" int cvh_gemm_bf16_nt(void* y, const void* x, const void* w, int64_t M
                        static_cast<uint16_t*>(y), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
                        static_cast<int>(M), N, K);
     return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+}
+
+namespace cvh {
+namespace {
+// Measured fastest SwiGLU-epilogue configuration for the Qwen3-0.6B gate/up shape (I = 3072,
+// K = 1024) per row-count bucket (64 x 32 tiles up to 64 rows, 32 x 64 up to 128, 64 x 128 above);
+// other shapes take 32 x 64 tiles.
+const GemmCfg* auto_swiglu_cfg(int64_t M, int I, int K) {
+    if (I == 3072 && K == 1024) return find_swiglu_cfg(M <= 64 ? 321241 : M <= 128 ? 321222 : 322422);
+    return find_swiglu_cfg(321222);
+}
+}  // namespace
+}  // namespace cvh
+
+extern "C" int cvh_gemm_bf16_nt_swiglu(void* act, const void* x, const void* w, int64_t M, int I, int K, int config,
+                                       cvh_stream_t stream) {
+    using namespace cvh;
+    if (M < 0 || I <= 0 || K <= 0) return CVH_ERR_INVALID_ARG;
+    if (M == 0) return CVH_OK;
+    if (!act || !x || !w) return CVH_ERR_INVALID_ARG;
+    if (M > (1 << 20) || I % 16 || K % kChunk || I > (1 << 29)) return CVH_ERR_UNSUPPORTED;
+    const int N = 2 * I;
+    const GemmCfg* cfg = config > 0 ? find_swiglu_cfg(config) : auto_swiglu_cfg(M, I, K);
+    if (!cfg || N % cfg->bn()) return CVH_ERR_UNSUPPORTED;
+    const dim3 grid(N / cfg->bn(), static_cast<unsigned>((M + cfg->bm() - 1) / cfg->bm()));
+    hipLaunchKernelGGL(cfg->fn, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<uint16_t*>(act), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                       static_cast<int>(M), N, K);
+    return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+}
+
+extern "C" int cvh_gemm_bf16_nt_swiglu_config(int64_t M, int I, int K) {
+    const cvh::GemmCfg* c = cvh::auto_swiglu_cfg(M, I, K);
+    return c ? c->code() : 0;
+}
+
+extern "C" int cvh_gemm_bf16_nt_swiglu_configs(int* codes, int capacity) {
+    int n = 0;
+    for (const cvh::GemmCfg& c : cvh::kSwigluCfgs) {
+        if (codes && n < capacity) codes[n] = c.code();
+        ++n;
+    }
+    return n;
 }
 
 extern "C" int cvh_gemm_bf16_nt_configs(int* codes, int capacity) {

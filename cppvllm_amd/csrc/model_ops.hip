@@ -27,12 +27,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ u32x4 ld_nt(const void* p) { return __builtin_nontemporal_load(static_cast<const u32x4*>(p)); }
 
 // ---- SwiGLU ---------------------------------------------------------------------------------
-template <int DT>
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    const double e = exp(-static_cast<double>(g));
-    const float silu = Elem<DT>::load(Elem<DT>::store(static_cast<float>(static_cast<double>(g) / (1.0 + e))));
-    return silu * u;
-}
 
 // One thread per 8 consecutive outputs of a row (I % 8 == 0): two 16-byte loads (gate, up) and
 // one 16-byte store for 16-bit types.

@@ -262,3 +262,34 @@ def linear(out, x, w, config: int = 0) -> None:
         raise ValueError(f"linear: shapes x {tuple(x.shape)}, w {tuple(w.shape)}, out {tuple(out.shape)}")
     check("gemm_bf16_nt", _lib.lib().cvh_gemm_bf16_nt(out.data_ptr(), x.data_ptr(), w.data_ptr(), M, N, K,
                                                       int(config), _stream(out)))
+
+
+def interleave_gate_up(w_gate_up: torch.Tensor) -> torch.Tensor:
+    """[2I, K] gate-then-up weight rows -> the 16-row interleaved layout linear_swiglu takes."""
+    n, k = w_gate_up.shape
+    i = n // 2
+    if n % 32:
+        raise ValueError("interleave_gate_up: 2I must be a multiple of 32")
+    return w_gate_up.view(2, i // 16, 16, k).transpose(0, 1).reshape(n, k).contiguous()
+
+
+def deinterleave_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """Inverse of interleave_gate_up: interleaved [2I, K] rows -> gate rows then up rows."""
+    n, k = w.shape
+    return w.view(n // 32, 2, 16, k).transpose(0, 1).reshape(n, k).contiguous()
+
+
+def linear_swiglu(act, x, w_interleaved, config: int = 0) -> None:
+    """act [M, I] = swiglu(x . w^T) with w's gate/up rows interleaved by 16 (at::linear +
+    fused::swiglu, model/model_architecture.cpp:182-184) in one gfx950 kernel."""
+    M = x.size(0)
+    if M == 0:
+        return
+    _require_cuda(act, x, w_interleaved)
+    if not (x.dtype == w_interleaved.dtype == act.dtype == torch.bfloat16):
+        raise ValueError("linear_swiglu: bf16 tensors only")
+    N, K = w_interleaved.shape
+    if x.size(1) != K or tuple(act.shape) != (M, N // 2):
+        raise ValueError(f"linear_swiglu: shapes x {tuple(x.shape)}, w {tuple(w_interleaved.shape)}, act {tuple(act.shape)}")
+    check("gemm_bf16_nt_swiglu", _lib.lib().cvh_gemm_bf16_nt_swiglu(act.data_ptr(), x.data_ptr(), w_interleaved.data_ptr(),
+                                                                    M, N // 2, K, int(config), _stream(act)))

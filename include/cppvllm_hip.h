@@ -297,6 +297,22 @@ int cvh_gemm_bf16_nt_config(int64_t M, int N, int K);
  * and returns the count. */
 int cvh_gemm_bf16_nt_configs(int* codes, int capacity);
 
+/* Gate/up projection with the SwiGLU epilogue: act[M][I] = swiglu(x[M][K] . w[2I][K]^T), where w's
+ * rows are the gate and up weight rows interleaved in blocks of 16 (rows 32b..32b+15 = gate rows
+ * 16b..16b+15, rows 32b+16..32b+31 = up rows 16b..16b+15). Each product is rounded to bf16 and the
+ * SwiGLU is cvh_swiglu's arithmetic, so act equals cvh_gemm_bf16_nt with the same config on the
+ * same interleaved w, de-interleaved, followed by cvh_swiglu, bit for bit.
+ * Replaces: at::linear(x, L.w_gate_up) + fused::swiglu(act, gu)
+ *           (model/model_architecture.cpp:182-184, kernels/fused_ops.cu:209-220).
+ * Requires I % 16 == 0, K % 128 == 0. config: 0 = automatic, otherwise a tiled code listed by
+ * cvh_gemm_bf16_nt_swiglu_configs. */
+int cvh_gemm_bf16_nt_swiglu(void* act, const void* x, const void* w, int64_t M, int I, int K, int config,
+                            cvh_stream_t stream);
+/* The configuration cvh_gemm_bf16_nt_swiglu picks for config == 0. */
+int cvh_gemm_bf16_nt_swiglu_config(int64_t M, int I, int K);
+/* Codes of the compiled SwiGLU-epilogue configurations (as cvh_gemm_bf16_nt_configs). */
+int cvh_gemm_bf16_nt_swiglu_configs(int* codes, int capacity);
+
 /* Library version string (static storage). */
 const char* cvh_version(void);
 

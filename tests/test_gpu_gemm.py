@@ -13,11 +13,11 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _codes():
-    L = _lib.lib()
-    n = L.cvh_gemm_bf16_nt_configs(None, 0)
+def _codes(fn="cvh_gemm_bf16_nt_configs"):
+    f = getattr(_lib.lib(), fn)
+    n = f(None, 0)
     buf = (C.c_int * n)()
-    L.cvh_gemm_bf16_nt_configs(buf, n)
+    f(buf, n)
     return list(buf)
 
 
@@ -85,6 +85,29 @@ def test_auto_dispatch_qwen_shapes(name):
         ops.linear(y, x.to(DEV), w.to(DEV))
         torch.cuda.synchronize()
         _check(y, x, w)
+
+
+@pytest.mark.parametrize("code", [0] + _codes("cvh_gemm_bf16_nt_swiglu_configs"))
+def test_swiglu_epilogue_bitexact(code):
+    """Fused gate/up GEMM + SwiGLU == the same tiled GEMM, de-interleaved, then cvh_swiglu."""
+    I, K = 512, 384
+    for M in (1, 37, 130):
+        say(f"gemm swiglu config {code} M={M} I={I} K={K}")
+        x, w = _inputs(M, 2 * I, K, code + M)
+        x = (x.float() * 2).to(torch.bfloat16)                 # gate values well into silu's curve
+        wi = ops.interleave_gate_up(w).to(DEV)
+        xd = x.to(DEV)
+        act = torch.empty((M, I), dtype=torch.bfloat16, device=DEV)
+        ops.linear_swiglu(act, xd, wi, code)
+        plain = code if code else _lib.lib().cvh_gemm_bf16_nt_swiglu_config(M, I, K)
+        gu_il = torch.empty((M, 2 * I), dtype=torch.bfloat16, device=DEV)
+        ops.linear(gu_il, xd, wi, plain)
+        gu = ops.deinterleave_gate_up(gu_il.t().contiguous()).t().contiguous()
+        want = torch.empty_like(act)
+        ops.fused.swiglu(want, gu)
+        torch.cuda.synchronize()
+        assert torch.equal(act.view(torch.int16), want.view(torch.int16))
+        _check(gu, x, w)
 
 
 def test_lm_head_shape():
