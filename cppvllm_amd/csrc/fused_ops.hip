@@ -64,6 +64,11 @@ __global__ __launch_bounds__(64 * kNormWaves) void rms_norm_kernel(typename Elem
     T* rr = ADD ? resid + row * dim : nullptr;
     T* orow = out + row * dim;
 
+    // the gains are loaded with the row, so the kernel waits for memory once
+    T wr[MAXC][8];
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+        if (lane + 64 * j < nchunk) C::load(w + (lane + 64 * j) * 8, wr[j]);
     float v[MAXC][8];
     float ss = 0.f;
 #pragma unroll
@@ -95,12 +100,11 @@ __global__ __launch_bounds__(64 * kNormWaves) void rms_norm_kernel(typename Elem
     for (int j = 0; j < MAXC; ++j) {
         const int c = lane + 64 * j;
         if (c < nchunk) {
-            T wr[8], o[8];
-            C::load(w + c * 8, wr);
+            T o[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float n = E::load(E::store(v[j][e] * inv));
-                o[e] = E::store(n * E::load(wr[e]));
+                o[e] = E::store(n * E::load(wr[j][e]));
             }
             C::store(orow + c * 8, o);
         }
@@ -131,16 +135,32 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     const uint16_t* src = qkv + (t * n_tasks + task) * HD;
     const int e0 = P * gl;               // first-half element index; partner is e0 + HALF
 
-    float x[2 * P];
+    // every global input of the task is requested before the first reduction, so the kernel waits
+    // for memory once: the head, and for Q/K the norm gains and this position's cos/sin
+    const int64_t slot = slots[t];
+    const int64_t pos = positions[t];
+    const bool is_qk = task < H + KV;
+    float x[2 * P], wv[2 * P], cs[P], sn[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) {
         x[j] = bf16_bits_to_f32(src[e0 + j]);
         x[P + j] = bf16_bits_to_f32(src[HALF + e0 + j]);
     }
-    const int64_t slot = slots[t];
+    if (is_qk) {
+        const uint16_t* wn = task < H ? q_norm : k_norm;
+        const float* cr = cos_t + pos * HALF + e0;
+        const float* sr = sin_t + pos * HALF + e0;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            wv[j] = bf16_bits_to_f32(wn[e0 + j]);
+            wv[P + j] = bf16_bits_to_f32(wn[HALF + e0 + j]);
+            cs[j] = cr[j];
+            sn[j] = sr[j];
+        }
+    }
     const int bs_mask = (1 << log2_bs) - 1;
 
-    if (task >= H + KV) {                // ---- V: quantise (kernels/fused_ops.cu:125-143)
+    if (!is_qk) {                        // ---- V: quantise (kernels/fused_ops.cu:125-143)
         const int kvh = task - H - KV;
         float amax = 0.f;
 #pragma unroll
@@ -173,7 +193,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
 
     // ---- Q / K: per-head RMSNorm (kernels/fused_ops.cu:145-156)
     const bool is_q = task < H;
-    const uint16_t* wn = is_q ? q_norm : k_norm;
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 2 * P; ++j) ss = ss + x[j] * x[j];
@@ -183,17 +202,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     float n[2 * P];
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-        n[j] = round_bf16(round_bf16(x[j] * inv) * bf16_bits_to_f32(wn[e0 + j]));
-        n[P + j] = round_bf16(round_bf16(x[P + j] * inv) * bf16_bits_to_f32(wn[HALF + e0 + j]));
+        n[j] = round_bf16(round_bf16(x[j] * inv) * wv[j]);
+        n[P + j] = round_bf16(round_bf16(x[P + j] * inv) * wv[P + j]);
     }
     // ---- neox RoPE on (e, e+HALF) (kernels/fused_ops.cu:157-166)
-    const int64_t pos = positions[t];
-    const float* cr = cos_t + pos * HALF + e0;
-    const float* sr = sin_t + pos * HALF + e0;
     float r[2 * P];
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-        const float c = cr[j], s = sr[j];
+        const float c = cs[j], s = sn[j];
         const float a = n[j], b = n[P + j];
         const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
         r[j] = ac - bs;
