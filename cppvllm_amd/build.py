@@ -33,7 +33,7 @@ SOURCES = {
     "fused_ops.hip": ["-ffp-contract=off"],
     "paged_attention.hip": [],
     "paged_prefill.hip": [],
-    "gemm.hip": [],
+    "gemm.hip": ["-ffp-contract=off"],
     "batch_metadata.hip": ["-ffp-contract=off"],
     "model_ops.hip": ["-ffp-contract=off"],
 }

@@ -13,11 +13,12 @@ namespace cvh {
 
 // ---- bf16 ------------------------------------------------------------------------------------
 // float -> bf16 bits, round to nearest even; NaN -> quiet NaN with the sign kept.
+// Branch-free (both results computed, one selected), so a wave never splits on a NaN test.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t qnan = (u >> 16) | 0x40u;
+    return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }

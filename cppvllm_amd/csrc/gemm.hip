@@ -42,6 +42,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
+
 // W operand of one chunk for one wave: lane (i16, g) holds k = 32s + 8g .. +8 of row i16 at step s,
 // so each load instruction reads 64 contiguous bytes of each of the wave's 16 rows.
 struct WChunk {
@@ -381,8 +382,79 @@ __device__ __forceinline__ void wait_stages(int ahead) {
     }
 }
 
-// Epilogues of the tiled kernel.
+// Epilogues of the tiled kernels.
 enum { kEpiStore = 0, kEpiSwiglu = 1 };
+
+// One 128-k chunk of a wave's MF x NF fragments from LDS chunk tiles (rows of 256 B, 16-byte
+// pieces stored at slot p ^ (row & 15)): xs points at the wave's first X row, ws at its first W row.
+template <int MF, int NF>
+__device__ __forceinline__ void chunk_mma(f32x4_t (&acc)[MF][NF], const uint8_t* xs, const uint8_t* ws, int i16,
+                                          int g) {
+    constexpr int kRowBytes = kChunk * 2;
+#pragma unroll
+    for (int s = 0; s < kChunk / 32; ++s) {
+        const int sl = ((4 * s + g) ^ i16) * 16;
+        u32x4_t a[NF], b[MF];
+#pragma unroll
+        for (int e = 0; e < NF; ++e) a[e] = *reinterpret_cast<const u32x4_t*>(ws + (e * 16 + i16) * kRowBytes + sl);
+#pragma unroll
+        for (int f = 0; f < MF; ++f) b[f] = *reinterpret_cast<const u32x4_t*>(xs + (f * 16 + i16) * kRowBytes + sl);
+#pragma unroll
+        for (int f = 0; f < MF; ++f)
+#pragma unroll
+            for (int e = 0; e < NF; ++e)
+                acc[f][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[e]),
+                                                                    __builtin_bit_cast(bf16x8_t, b[f]), acc[f][e], 0, 0,
+                                                                    0);
+    }
+}
+
+// Stores a wave's fragments: kEpiStore writes y [M][N] in bf16; kEpiSwiglu reads fragment pairs
+// (e, e+1) as gate and up of the same outputs (W rows interleaved in blocks of 16) and writes
+// act = y [M][N/2] with the SwiGLU kernel's arithmetic, the products rounded to bf16 first as the
+// reference's gate_up tensor is.
+template <int MF, int NF, int WN, int EPI>
+__device__ __forceinline__ void tile_epilogue(const f32x4_t (&acc)[MF][NF], uint16_t* __restrict__ y, int M, int N,
+                                              int m0, int n0, int wm, int wn, int i16, int g) {
+    if constexpr (EPI == kEpiStore) {
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int m = m0 + (wm * MF + f) * 16 + i16;
+            if (m >= M) continue;
+#pragma unroll
+            for (int e = 0; e < NF; ++e) {
+                uint2 v;
+                v.x = pack_bf16x2(acc[f][e][0], acc[f][e][1]);
+                v.y = pack_bf16x2(acc[f][e][2], acc[f][e][3]);
+                *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * N + n0 + (wn * NF + e) * 16 + 4 * g) = v;
+            }
+        }
+    } else {
+        // W rows interleaved in blocks of 16 (gate j..j+15, then up j..j+15): fragment pair
+        // (e, e+1) of a lane holds gate and up of the same 4 outputs. y is act [M][N/2]; the
+        // products are rounded to bf16 first, as the reference's gate_up tensor is.
+        static_assert(NF % 2 == 0, "gate/up fragment pairs");
+        const int I = N >> 1;
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int m = m0 + (wm * MF + f) * 16 + i16;
+            if (m >= M) continue;
+#pragma unroll
+            for (int e = 0; e < NF; e += 2) {
+                const int j = ((n0 + (wn * NF + e) * 16) >> 1) + 4 * g;
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    o[r] = silu_mul<CVH_DTYPE_BF16>(round_bf16(acc[f][e][r]), round_bf16(acc[f][e + 1][r]));
+                uint2 v;
+                v.x = pack_bf16x2(o[0], o[1]);
+                v.y = pack_bf16x2(o[2], o[3]);
+                *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * I + j) = v;
+            }
+        }
+    }
+}
+
 
 template <int MF, int NF, int WM, int WN, int S, int EPI = kEpiStore>
 __global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
@@ -437,62 +509,9 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ 
         asm volatile("" ::: "memory");
         if (c + kStages - 1 < nc) issue(c + kStages - 1, (c + kStages - 1) % kStages);
         const uint8_t* st = lds + (c % kStages) * kStageBytes;
-        const uint8_t* xs = st + (wm * MF * 16) * kRowBytes;
-        const uint8_t* ws = st + (BM + wn * NF * 16) * kRowBytes;
-#pragma unroll
-        for (int s = 0; s < kChunk / 32; ++s) {
-            const int sl = ((4 * s + g) ^ i16) * 16;
-            u32x4_t a[NF], b[MF];
-#pragma unroll
-            for (int e = 0; e < NF; ++e) a[e] = *reinterpret_cast<const u32x4_t*>(ws + (e * 16 + i16) * kRowBytes + sl);
-#pragma unroll
-            for (int f = 0; f < MF; ++f) b[f] = *reinterpret_cast<const u32x4_t*>(xs + (f * 16 + i16) * kRowBytes + sl);
-#pragma unroll
-            for (int f = 0; f < MF; ++f)
-#pragma unroll
-                for (int e = 0; e < NF; ++e)
-                    acc[f][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[e]),
-                                                                        __builtin_bit_cast(bf16x8_t, b[f]), acc[f][e],
-                                                                        0, 0, 0);
-        }
+        chunk_mma<MF, NF>(acc, st + (wm * MF * 16) * kRowBytes, st + (BM + wn * NF * 16) * kRowBytes, i16, g);
     }
-    if constexpr (EPI == kEpiStore) {
-#pragma unroll
-        for (int f = 0; f < MF; ++f) {
-            const int m = m0 + (wm * MF + f) * 16 + i16;
-            if (m >= M) continue;
-#pragma unroll
-            for (int e = 0; e < NF; ++e) {
-                uint2 v;
-                v.x = pack_bf16x2(acc[f][e][0], acc[f][e][1]);
-                v.y = pack_bf16x2(acc[f][e][2], acc[f][e][3]);
-                *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * N + n0 + (wn * NF + e) * 16 + 4 * g) = v;
-            }
-        }
-    } else {
-        // W rows interleaved in blocks of 16 (gate j..j+15, then up j..j+15): fragment pair
-        // (e, e+1) of a lane holds gate and up of the same 4 outputs. y is act [M][N/2]; the
-        // products are rounded to bf16 first, as the reference's gate_up tensor is.
-        static_assert(NF % 2 == 0, "gate/up fragment pairs");
-        const int I = N >> 1;
-#pragma unroll
-        for (int f = 0; f < MF; ++f) {
-            const int m = m0 + (wm * MF + f) * 16 + i16;
-            if (m >= M) continue;
-#pragma unroll
-            for (int e = 0; e < NF; e += 2) {
-                const int j = ((n0 + (wn * NF + e) * 16) >> 1) + 4 * g;
-                float o[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    o[r] = silu_mul<CVH_DTYPE_BF16>(round_bf16(acc[f][e][r]), round_bf16(acc[f][e + 1][r]));
-                uint2 v;
-                v.x = pack_bf16x2(o[0], o[1]);
-                v.y = pack_bf16x2(o[2], o[3]);
-                *reinterpret_cast<uint2*>(y + static_cast<size_t>(m) * I + j) = v;
-            }
-        }
-    }
+    tile_epilogue<MF, NF, WN, EPI>(acc, y, M, N, m0, n0, wm, wn, i16, g);
 }
 
 typedef void (*GemmFn)(uint16_t*, const uint16_t*, const uint16_t*, int, int, int);
@@ -535,6 +554,7 @@ const GemmCfg kCfgs[] = {
     CVH_GEMM_TILE(2, 1, 2, 2, 3), CVH_GEMM_TILE(1, 2, 2, 2, 3), CVH_GEMM_TILE(2, 2, 2, 2, 3),
     CVH_GEMM_TILE(2, 1, 4, 1, 3), CVH_GEMM_TILE(1, 2, 1, 4, 3), CVH_GEMM_TILE(4, 1, 1, 4, 3),
     CVH_GEMM_TILE(2, 4, 2, 2, 3), CVH_GEMM_TILE(4, 2, 2, 2, 3), CVH_GEMM_TILE(1, 2, 4, 1, 3),
+    CVH_GEMM_TILE(2, 1, 1, 4, 3), CVH_GEMM_TILE(2, 2, 1, 4, 3),
     CVH_GEMM_TILE(1, 1, 2, 2, 0), CVH_GEMM_TILE(1, 1, 4, 1, 0), CVH_GEMM_TILE(2, 1, 2, 2, 0),
 };
 #undef CVH_GEMM_CFG
@@ -547,6 +567,7 @@ const GemmCfg kCfgs[] = {
 const GemmCfg kSwigluCfgs[] = {
     CVH_GEMM_SWIGLU(1, 2, 2, 2, 3), CVH_GEMM_SWIGLU(2, 2, 2, 2, 3), CVH_GEMM_SWIGLU(2, 4, 2, 2, 3),
     CVH_GEMM_SWIGLU(1, 2, 1, 4, 3), CVH_GEMM_SWIGLU(1, 2, 4, 1, 3), CVH_GEMM_SWIGLU(4, 2, 2, 2, 3),
+    CVH_GEMM_SWIGLU(2, 2, 1, 4, 3),
 };
 #undef CVH_GEMM_SWIGLU
 
