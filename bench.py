@@ -288,6 +288,95 @@ def run_fused(args):
     }
 
 
+GEMM_SHAPES = {"qkv": (4096, 1024), "o_proj": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072),
+               "lm_head": (151936, 1024)}
+
+
+def run_gemm(args):
+    """Decode-projection GEMMs of Qwen3-0.6B: hipBLASLt (torch.mm) vs cvh_gemm_bf16_nt's automatic
+    configuration (and, with --gemm-all, every compiled configuration) per row count, plus the gate/up
+    GEMM with the SwiGLU epilogue. HIP-graph replay of back-to-back calls cycling distinct weight
+    copies (48, or 2 for the lm_head) so the weights come from HBM as in a 28-layer step."""
+    import ctypes as C
+
+    import torch
+
+    from cppvllm_amd import _lib, ops
+    L = _lib.lib()
+    dev = "cuda"
+
+    def codes(fn):
+        n = fn(None, 0)
+        b = (C.c_int * n)()
+        fn(b, n)
+        return list(b)
+
+    def timed(body, reps):
+        body()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                body()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / 5 / reps
+
+    rows = [1, 8, 16, 32, 48, 64, 96, 128, 192, 256]
+    every = codes(L.cvh_gemm_bf16_nt_configs)
+    res = {"metric": "decode-projection GEMM us per call", "unit": "us", "rows": rows, "shapes": {}}
+    for name, (N, K) in GEMM_SHAPES.items():
+        ws = [(torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(2 if N > 100000 else 48)]
+        per = {}
+        for M in rows:
+            x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+            y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+            auto = L.cvh_gemm_bf16_nt_config(M, N, K)
+            ent = {"hipblaslt": timed(lambda: [torch.mm(x, w.t(), out=y) for w in ws], len(ws)),
+                   "auto_code": auto,
+                   "auto": timed(lambda: [ops.linear(y, x, w) for w in ws], len(ws))}
+            if args.gemm_all:
+                cand = {}
+                for c in every:
+                    if L.cvh_gemm_bf16_nt(y.data_ptr(), x.data_ptr(), ws[0].data_ptr(), M, N, K, c,
+                                          torch.cuda.current_stream().cuda_stream) != 0:
+                        continue            # tile or K split does not fit this shape
+                    cand[c] = timed(lambda: [ops.linear(y, x, w, c) for w in ws], len(ws))
+                ent["best_code"], ent["best"] = min(cand.items(), key=lambda kv: kv[1])
+            ent["weight_gbs"] = N * K * 2 / ent["auto"] / 1e3
+            per[M] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in ent.items()}
+            print(f"bench: {name} M={M} " + " ".join(f"{k}={v}" for k, v in per[M].items()), flush=True,
+                  file=sys.stderr)
+        res["shapes"][f"{name} ({N}x{K})"] = per
+        del ws
+    I, K = 3072, 1024
+    ws = [(torch.randn(2 * I, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(48)]
+    per = {}
+    for M in rows:
+        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        gu = torch.empty(M, 2 * I, device=dev, dtype=torch.bfloat16)
+        act = torch.empty(M, I, device=dev, dtype=torch.bfloat16)
+
+        def unfused():
+            for w in ws:
+                torch.mm(x, w.t(), out=gu)
+                ops.fused.swiglu(act, gu)
+        per[M] = {"hipblaslt_plus_swiglu": round(timed(unfused, len(ws)), 3),
+                  "auto_code": L.cvh_gemm_bf16_nt_swiglu_config(M, I, K),
+                  "fused": round(timed(lambda: [ops.linear_swiglu(act, x, w) for w in ws], len(ws)), 3)}
+        print(f"bench: gate_up+swiglu M={M} {per[M]}", flush=True, file=sys.stderr)
+    res["shapes"]["gate_up + SwiGLU epilogue (6144x1024 -> 3072)"] = per
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -310,6 +399,9 @@ def main():
     ap.add_argument("--prefill", action="store_true", help="time the MFMA multi-query (prefill) kernel alone")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end leg of the default run")
     ap.add_argument("--e2e-block-size", type=int, default=256)
+    ap.add_argument("--gemm", action="store_true",
+                    help="decode-projection GEMMs: hipBLASLt vs cvh_gemm_bf16_nt per row count")
+    ap.add_argument("--gemm-all", action="store_true", help="with --gemm: also time every compiled configuration")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 3 plain 1 GiB device-to-device copies (rocprofv3 FETCH/WRITE_SIZE scale)")
     args = ap.parse_args()
@@ -330,6 +422,9 @@ def main():
         return
     if args.prefill:
         print(json.dumps(run_prefill(args)), flush=True)
+        return
+    if args.gemm:
+        print(json.dumps(run_gemm(args)), flush=True)
         return
     if args.config == 2:
         print(json.dumps(run_fused(args)), flush=True)
