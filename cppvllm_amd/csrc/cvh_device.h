@@ -50,6 +50,114 @@ template <> struct Elem<CVH_DTYPE_F32> {
     static __device__ __forceinline__ T store(float f) { return f; }
 };
 
+// ---- RMSNorm of one row by one wavefront ---------------------------------------------------------
+// 8-element chunks through 16-byte accesses (two for f32).
+template <typename T> struct Chunk8;
+template <> struct Chunk8<uint16_t> {
+    static __device__ __forceinline__ void load(const uint16_t* p, uint16_t (&v)[8]) {
+        const uint4 u = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { v[2 * i] = w[i] & 0xffffu; v[2 * i + 1] = w[i] >> 16; }
+    }
+    static __device__ __forceinline__ void store(uint16_t* p, const uint16_t (&v)[8]) {
+        uint4 u;
+        u.x = v[0] | (uint32_t(v[1]) << 16); u.y = v[2] | (uint32_t(v[3]) << 16);
+        u.z = v[4] | (uint32_t(v[5]) << 16); u.w = v[6] | (uint32_t(v[7]) << 16);
+        *reinterpret_cast<uint4*>(p) = u;
+    }
+};
+template <> struct Chunk8<float> {
+    static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    static __device__ __forceinline__ void store(float* p, const float (&v)[8]) {
+        reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+};
+
+// How a row's input x is read: plainly, or with agent-scope coherent loads (relaxed atomics, the
+// sc1 bit) when another workgroup of the same kernel wrote it (see the GEMM's fused norm).
+struct PlainChunk {
+    template <typename T>
+    __device__ __forceinline__ void operator()(const T* p, T (&v)[8]) const { Chunk8<T>::load(p, v); }
+};
+struct AgentChunk {
+    __device__ __forceinline__ void operator()(const uint16_t* p, uint16_t (&v)[8]) const {
+        const uint64_t a = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = static_cast<uint16_t>(a >> (16 * i));
+            v[4 + i] = static_cast<uint16_t>(b >> (16 * i));
+        }
+    }
+};
+
+// RMSNorm (ADD: after resid <- rnd(resid + x), normalising resid) of one row of `dim` elements
+// (dim % 8 == 0, dim <= 512 * MAXC) by the 64 lanes of a wave: lane l owns chunks l, l+64, ...;
+// the sum of squares runs over the lane's elements in index order, then an xor butterfly over the
+// 64 lanes; inv = 1 / sqrt(ss / dim + eps) with IEEE sqrt and division; out = rnd(rnd(v * inv) * w).
+// Every input is requested before the first reduction. Translation units using this are built
+// without FMA contraction.
+template <int DT, bool ADD, int MAXC, typename XLoad>
+__device__ __forceinline__ void norm_row(typename Elem<DT>::T* __restrict__ orow, typename Elem<DT>::T* rr,
+                                         const typename Elem<DT>::T* xr, const typename Elem<DT>::T* __restrict__ w,
+                                         int dim, float eps, int lane, XLoad xload) {
+    using E = Elem<DT>;
+    using T = typename E::T;
+    using C = Chunk8<T>;
+    const int nchunk = dim >> 3;
+    T wr[MAXC][8];
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+        if (lane + 64 * j < nchunk) C::load(w + (lane + 64 * j) * 8, wr[j]);
+    float v[MAXC][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+            T raw[8];
+            xload(xr + c * 8, raw);
+            if constexpr (ADD) {
+                T rs[8];
+                C::load(rr + c * 8, rs);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) rs[e] = E::store(E::load(rs[e]) + E::load(raw[e]));
+                C::store(rr + c * 8, rs);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) raw[e] = rs[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[j][e] = E::load(raw[e]);
+                ss = ss + v[j][e] * v[j][e];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss = ss + __shfl_xor(ss, m, 64);
+    const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nchunk) {
+            T o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float n = E::load(E::store(v[j][e] * inv));
+                o[e] = E::store(n * E::load(wr[j][e]));
+            }
+            C::store(orow + c * 8, o);
+        }
+    }
+}
+
 // ---- SwiGLU element ---------------------------------------------------------------------------
 // silu(g) * u with the reference's rounding points (kernels/fused_ops.cu:210-219): silu rounded to
 // the storage type, the product left for the caller to round. The exponential is evaluated in

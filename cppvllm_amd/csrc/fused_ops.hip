@@ -21,94 +21,16 @@ namespace {
 // keeps them in registers between the sum-of-squares pass and the output pass.
 constexpr int kNormWaves = 4;
 
-template <typename T> struct Chunk8;
-template <> struct Chunk8<uint16_t> {
-    static __device__ __forceinline__ void load(const uint16_t* p, uint16_t (&v)[8]) {
-        const uint4 u = *reinterpret_cast<const uint4*>(p);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { v[2 * i] = w[i] & 0xffffu; v[2 * i + 1] = w[i] >> 16; }
-    }
-    static __device__ __forceinline__ void store(uint16_t* p, const uint16_t (&v)[8]) {
-        uint4 u;
-        u.x = v[0] | (uint32_t(v[1]) << 16); u.y = v[2] | (uint32_t(v[3]) << 16);
-        u.z = v[4] | (uint32_t(v[5]) << 16); u.w = v[6] | (uint32_t(v[7]) << 16);
-        *reinterpret_cast<uint4*>(p) = u;
-    }
-};
-template <> struct Chunk8<float> {
-    static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
-        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    }
-    static __device__ __forceinline__ void store(float* p, const float (&v)[8]) {
-        reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
-        reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
-    }
-};
-
 template <int DT, bool ADD, int MAXC>
 __global__ __launch_bounds__(64 * kNormWaves) void rms_norm_kernel(typename Elem<DT>::T* __restrict__ out,
                                                                    typename Elem<DT>::T* resid,
                                                                    const typename Elem<DT>::T* __restrict__ x,
                                                                    const typename Elem<DT>::T* __restrict__ w,
                                                                    int64_t num_rows, int dim, float eps) {
-    using E = Elem<DT>;
-    using T = typename E::T;
-    using C = Chunk8<T>;
-    const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kNormWaves + (threadIdx.x >> 6);
     if (row >= num_rows) return;
-    const int nchunk = dim >> 3;
-    const T* xr = x + row * dim;
-    T* rr = ADD ? resid + row * dim : nullptr;
-    T* orow = out + row * dim;
-
-    // the gains are loaded with the row, so the kernel waits for memory once
-    T wr[MAXC][8];
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j)
-        if (lane + 64 * j < nchunk) C::load(w + (lane + 64 * j) * 8, wr[j]);
-    float v[MAXC][8];
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nchunk) {
-            T raw[8];
-            C::load(xr + c * 8, raw);
-            if constexpr (ADD) {
-                T rs[8];
-                C::load(rr + c * 8, rs);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) rs[e] = E::store(E::load(rs[e]) + E::load(raw[e]));
-                C::store(rr + c * 8, rs);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) raw[e] = rs[e];
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                v[j][e] = E::load(raw[e]);
-                ss = ss + v[j][e] * v[j][e];
-            }
-        }
-    }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss = ss + shfl_xor(ss, m);
-    const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(dim) + eps);
-#pragma unroll
-    for (int j = 0; j < MAXC; ++j) {
-        const int c = lane + 64 * j;
-        if (c < nchunk) {
-            T o[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float n = E::load(E::store(v[j][e] * inv));
-                o[e] = E::store(n * E::load(wr[j][e]));
-            }
-            C::store(orow + c * 8, o);
-        }
-    }
+    norm_row<DT, ADD, MAXC>(out + row * dim, ADD ? resid + row * dim : nullptr, x + row * dim, w, dim, eps,
+                            threadIdx.x & 63, PlainChunk{});
 }
 
 // ---- QK-RMSNorm + RoPE + FP8 KV write --------------------------------------------------------
