@@ -391,6 +391,8 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4),
                     help="3: 256 seqs, ctx U(100,1024)+U(0,1024) (headline); 4: 64 seqs, ctx log-U(4k,32k); "
                          "2: the fused pre-attention ops over 4096 packed tokens")
+    ap.add_argument("--seqs", type=int, default=256,
+                    help="config 3 with this many sequences (a smaller decode batch; the headline is 256)")
     ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
     ap.add_argument("--no-shared-reuse", action="store_true",
                     help="config 4b without telling the plan which blocks are shared (all reads non-temporal)")
@@ -439,7 +441,7 @@ def main():
         return
     print(f"bench: building config {args.config} on device", flush=True, file=sys.stderr)
     if args.config == 3:
-        b = workloads.config3(device=dev)
+        b = workloads.config3(device=dev, seqs=args.seqs)
     else:
         b = workloads.config4(device=dev, shared_prefix=args.shared_prefix)
     lens = b["token_kv_len"].cpu().tolist()

@@ -177,7 +177,7 @@ template <typename T> __device__ __forceinline__ T ld_uniform(const T* ptr, int6
 // the physical blocks of its first two tiles, so a planned launch issues them before anything
 // else. row < 0: no preload.
 struct PlanRec {
-    int row, lt, le, kv_len, seq, b_ok, r_s, pad;
+    int row, lt, le, kv_len, seq, b_ok, r_s, r_e;   // r_e: one past the last row holding a tile of the range
     int64_t a_lo, a_hi, b_lo, b_hi;
 };
 
@@ -291,6 +291,19 @@ template <typename F> __device__ __forceinline__ int first_row(F pfx, int rows, 
     return r;
 }
 
+// One past the last row holding a tile of [u0, u1) (r_s when the range is empty): the rows a
+// workgroup stages q for and walks are [r_s, end_row).
+template <typename F> __device__ __forceinline__ int end_row(F pfx, int rows, int64_t u0, int64_t u1, int r_s) {
+    if (u1 <= u0) return r_s;
+    int lo = 0, hi = rows;               // last r with prefix[r] <= u1 - 1
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pfx(mid) <= u1 - 1) lo = mid;
+        else hi = mid;
+    }
+    return lo + 1;
+}
+
 // One piece of work of a workgroup: tiles [lt, le) of row `row` (token t, kv head g of this wave).
 // row < 0 marks "no more work" (its other fields are safe dummies: loads made for it use zero-size
 // descriptors, and its table lookups stay inside block-table row 0).
@@ -338,12 +351,26 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     struct Phys {
         int64_t lo, hi;
     };
+    // With whole tiles inside one block (block_size >= 32) consecutive tiles mostly share a block:
+    // the last (sequence, block) -> physical block pair is kept in scalar registers, so a tile in
+    // the same block as the previous lookup issues no load (7 of 8 tiles at 256-token blocks) and
+    // nothing later waits on one.
+    int64_t memo_seq = -1, memo_phys = 0;
+    int memo_blk = -1;
     auto lookup = [&](const Piece& pc, int tile) -> Phys {
         const int64_t seq = static_cast<int64_t>(uniform(static_cast<int>(pc.seq)));
         const int64_t* table = p.block_tables + seq * p.table_width;
         const int p0 = uniform(tile * kTileKeys);
+        if constexpr (ONE_BLOCK) {
+            const int blk = p0 >> log2_bs;
+            if (seq != memo_seq || blk != memo_blk) {
+                memo_phys = max(ld_uniform(table, blk), int64_t{0});
+                memo_seq = seq;
+                memo_blk = blk;
+            }
+            return {memo_phys, memo_phys};
+        }
         const int64_t lo = max(ld_uniform(table, p0 >> log2_bs), int64_t{0});
-        if constexpr (ONE_BLOCK) return {lo, lo};
         const int64_t hi = max(ld_uniform(table, uniform(min(p0 + kTileKeys / 2, pc.kv_len - 1) >> log2_bs)),
                                int64_t{0});
         return {lo, hi};
@@ -389,7 +416,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // workgroup derives them from token_kv_len itself (one memory round trip more, then the
     // block-table round trip before its first K/V load).
     bool preA = false, preB = false, preQ = false;
-    int plan_row = -1, plan_lt = 0, plan_rs = -1;
+    int plan_row = -1, plan_lt = 0, plan_rs = -1, plan_re = -1;
     char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens);
     constexpr int QB = REP * HD * 2;                 // bytes of one row's q slice for one wave
     constexpr int QL = (QB + 1023) / 1024;           // 16-byte loads per lane per row
@@ -400,10 +427,11 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         const PlanRec* rp = p.plan + w;
         plan_row = ld_uniform(&rp->row, 0);
         plan_rs = ld_uniform(&rp->r_s, 0);
+        plan_re = ld_uniform(&rp->r_e, 0);
         uint4 qv[kPreQRows][QL];
 #pragma unroll
         for (int r = 0; r < kPreQRows; ++r) {
-            const bool live = r < p.qrows && plan_rs + r < rows;
+            const bool live = r < p.qrows && plan_rs + r < plan_re;
             const int rr = live ? plan_rs + r : 0;
             const int t = rr / hg_count, g = (rr % hg_count) * wpg + wi;
             const auto rs = make_rsrc(p.q + (static_cast<int64_t>(t) * H + g * REP) * HD, live ? QB : 0);
@@ -430,10 +458,16 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             pc.seq = ld_uniform(&rp->seq, 0);
             pc.shared_keys = (SHARED && live) ? ld_uniform(p.shared_tok, pc.t) : 0;
             const bool b_ok = live && ld_uniform(&rp->b_ok, 0) != 0;
-            load_tile(pc, plan_lt, A, {ld_uniform(&rp->a_lo, 0), ld_uniform(&rp->a_hi, 0)}, live);
-            load_tile(pc, plan_lt + 1, B, {ld_uniform(&rp->b_lo, 0), ld_uniform(&rp->b_hi, 0)}, b_ok);
+            const int64_t a_lo = ld_uniform(&rp->a_lo, 0), b_lo = ld_uniform(&rp->b_lo, 0);
+            load_tile(pc, plan_lt, A, {a_lo, ld_uniform(&rp->a_hi, 0)}, live);
+            load_tile(pc, plan_lt + 1, B, {b_lo, ld_uniform(&rp->b_hi, 0)}, b_ok);
             preA = live;
             preB = b_ok;
+            if (ONE_BLOCK && live) {         // the newest tile's block seeds the lookup memo
+                memo_seq = uniform(static_cast<int>(pc.seq));
+                memo_blk = ((b_ok ? plan_lt + 1 : plan_lt) * kTileKeys) >> log2_bs;
+                memo_phys = b_ok ? b_lo : a_lo;
+            }
         }
 #pragma unroll
         for (int r = 0; r < kPreQRows; ++r)
@@ -458,8 +492,10 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const int64_t U = pfx(rows);
     const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
 
-    // ---- first row to visit
-    const int r_s = first_row(pfx, rows, u0);
+    // ---- first row to visit, and one past the last row holding a tile of the range (a planned
+    // launch has both in its plan record)
+    const int r_s = PLANNED ? plan_rs : first_row(pfx, rows, u0);
+    const int r_e = PLANNED ? plan_re : end_row(pfx, rows, u0, u1, r_s);
     // ---- empty rows of the range (kv_len <= 0): zero output (the reference would give 0/0)
     for (int r = r_s; r < rows; ++r) {
         const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
@@ -662,8 +698,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // ---- per batch: one tile stream over its pieces, two tiles in flight ahead of the one being
     // computed (register triple buffer, unrolled by three so no tile is copied between buffers)
     for (;;) {
-        if (rb >= rows || pfx(rb) >= u1) return;
-        const int rlim = min(rows, rb + p.qrows);
+        if (rb >= r_e || pfx(rb) >= u1) return;         // rlim > rb below: the loop always advances
+        const int rlim = min(r_e, rb + p.qrows);
         Piece pa_ = piece_from(rb, rlim);
         if (pa_.row >= 0) {
             int ta_ = pa_.lt;
@@ -824,6 +860,7 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* pla
         PlanRec rec = {};
         rec.row = -1;
         rec.r_s = r_s;
+        rec.r_e = end_row(pf, rows, u0, u1, r_s);
         for (int r = r_s; r < rlim; ++r) {
             const int64_t pr0 = prefix[r], pr1 = prefix[r + 1];
             if (pr0 >= u1) break;

@@ -146,9 +146,10 @@ def config3_lens(seed: int = 1003, S: int = 256) -> list[int]:
     return (a + b).tolist()
 
 
-def config3(device="cpu", per_tensor=False, seed=1003):
-    """Headline: 256 sequences, ctx = U{100..1024} + U{0..1024}, 256-token blocks."""
-    return decode_batch(config3_lens(seed), 256, seed, device, per_tensor)
+def config3(device="cpu", per_tensor=False, seed=1003, seqs: int = 256):
+    """Headline: 256 sequences, ctx = U{100..1024} + U{0..1024}, 256-token blocks (`seqs` other
+    than 256: the same distribution over fewer or more sequences, a smaller decode batch)."""
+    return decode_batch(config3_lens(seed, seqs), 256, seed, device, per_tensor)
 
 
 def config4_lens(seed: int = 1004, S: int = 64, lo: int = 4096, hi: int = 32768) -> list[int]:
