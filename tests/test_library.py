@@ -63,6 +63,57 @@ def test_argument_validation_without_device():
     assert lib.cvh_qk_norm_rope_kv_write_fp8(*[p] * 14, 4, 16, 8, 128, 20, 0, 1e-6, None) == unsup
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="passes dummy device pointers; CPU-only check")
+def test_gemm_argument_validation_without_device():
+    lib = _lib.lib()
+    ok, bad, unsup = _lib.CVH_OK, _lib.CVH_ERR_INVALID_ARG, _lib.CVH_ERR_UNSUPPORTED
+    p = C.c_void_p(16)
+    assert lib.cvh_gemm_bf16_nt(None, None, None, 0, 64, 256, 0, None) == ok           # M == 0: no-op
+    assert lib.cvh_gemm_bf16_nt(None, p, p, 4, 64, 256, 0, None) == bad
+    assert lib.cvh_gemm_bf16_nt(p, p, p, -1, 64, 256, 0, None) == bad
+    assert lib.cvh_gemm_bf16_nt(p, p, p, 4, 56, 256, 0, None) == unsup                 # N % 16
+    assert lib.cvh_gemm_bf16_nt(p, p, p, 4, 64, 200, 0, None) == unsup                 # K % 128
+    assert lib.cvh_gemm_bf16_nt(p, p, p, 4, 64, 256, 77, None) == unsup                # unknown code
+    assert lib.cvh_gemm_bf16_nt(p, p, p, 4, 64, 256, 10211, None) == unsup             # one-shot K fixed at 1024
+    assert lib.cvh_gemm_bf16_nt(p, p, p, 4, 48, 256, 324222, None) == unsup            # 64-wide tile, N = 48
+    assert lib.cvh_gemm_bf16_nt_swiglu(None, None, None, 0, 64, 256, 0, None) == ok
+    assert lib.cvh_gemm_bf16_nt_swiglu(p, p, p, 4, 40, 256, 0, None) == unsup          # I % 16
+    assert lib.cvh_gemm_bf16_nt_swiglu(p, p, p, 4, 64, 256, 11, None) == unsup         # not a SwiGLU code
+
+
+def _codes(fn):
+    n = fn(None, 0)
+    buf = (C.c_int * n)()
+    assert fn(buf, n) == n
+    return list(buf)
+
+
+def test_gemm_dispatch_tables():
+    """The automatic choice is a compiled configuration that fits the shape, for every projection
+    of Qwen3-0.6B and every decode batch size, and the generic fallback covers other shapes."""
+    lib = _lib.lib()
+    every = set(_codes(lib.cvh_gemm_bf16_nt_configs))
+    swiglu = set(_codes(lib.cvh_gemm_bf16_nt_swiglu_configs))
+    assert len(every) == lib.cvh_gemm_bf16_nt_configs(None, 0) and swiglu
+
+    def fits(code, N, K):
+        if code >= 100000:
+            return N % (16 * ((code // 100) % 10) * (code % 10)) == 0 and K % 128 == 0
+        nwn = code % 10
+        if code >= 10000:
+            return N % (16 * nwn) == 0 and K == (4 // nwn) * ((code // 100) % 100) * 128
+        return N % (16 * nwn) == 0 and K % ((4 // nwn) * 128) == 0
+
+    shapes = [(4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072), (151936, 1024), (512, 640), (96, 384)]
+    for N, K in shapes:
+        for M in (1, 2, 7, 8, 9, 16, 17, 33, 64, 65, 100, 128, 129, 200, 256, 1000, 4096):
+            c = lib.cvh_gemm_bf16_nt_config(M, N, K)
+            assert c in every and fits(c, N, K), (N, K, M, c)
+    for M in (1, 16, 64, 65, 128, 129, 256):
+        c = lib.cvh_gemm_bf16_nt_swiglu_config(M, 3072, 1024)
+        assert c in swiglu and fits(c, 6144, 1024), (M, c)
+
+
 def test_partition_policy_and_workspace_sizes():
     lib = _lib.lib()
     # headline decode (256 tokens, 8 kv heads = one 8-wave row group, 8 x 256-token blocks):
