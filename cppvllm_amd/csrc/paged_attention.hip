@@ -37,6 +37,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstddef>
 #include <type_traits>
 
 #include "cvh_device.h"
@@ -176,9 +177,18 @@ template <typename T> __device__ __forceinline__ T ld_uniform(const T* ptr, int6
 // (shared by every layer of a step): the first piece of the workgroup's first batch of rows and
 // the physical blocks of its first two tiles, so a planned launch issues them before anything
 // else. row < 0: no preload.
+constexpr int kPlanWin = 8;                // rows of a workgroup's window carried in its plan record
 struct PlanRec {
     int row, lt, le, kv_len, seq, b_ok, r_s, r_e;   // r_e: one past the last row holding a tile of the range
     int64_t a_lo, a_hi, b_lo, b_hi;
+    // win = 1: every prefix entry and token record the workgroup reads lies in the window below, so
+    // its launch needs neither the LDS copies of the prefix and token metadata nor the barrier
+    // that publishes them. pre[i] = prefix[min(r_s + i, rows)]; tok[j] = token metadata of token
+    // r_s / (n_kv / wpg) + j (clamped); U = prefix[rows].
+    int win, U;
+    int pre[kPlanWin + 1];
+    int tkl[kPlanWin], tsq[kPlanWin];
+    int pad[3];
 };
 
 struct Params {
@@ -438,6 +448,17 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 #pragma unroll
             for (int j = 0; j < QL; ++j) qv[r][j] = buf_load<uint4>(rs, lane * 16 + j * 1024);
         }
+        // the plan's row window, one entry per lane (lanes 0..8 prefix, 0..7 token records)
+        const auto rec_rs = make_rsrc(rp, sizeof(PlanRec));
+        const int wpre = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(
+                rec_rs, static_cast<int>(offsetof(PlanRec, pre)) + 4 * min(lane, kPlanWin), 0, 0));
+        const int wtkl = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(
+                rec_rs, static_cast<int>(offsetof(PlanRec, tkl)) + 4 * min(lane, kPlanWin - 1), 0, 0));
+        const int wtsq = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(
+                rec_rs, static_cast<int>(offsetof(PlanRec, tsq)) + 4 * min(lane, kPlanWin - 1), 0, 0));
+        const int wU = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(
+                rec_rs, static_cast<int>(offsetof(PlanRec, U)), 0, 0));
+        const bool win = ld_uniform(&rp->win, 0) != 0;
         const int bd = blockDim.x, tid = threadIdx.x;
         const auto pre_rs = make_rsrc(p.prefix_out, (rows + 1) * 4);
         const auto tok_rs = make_rsrc(p.plan_tok, p.num_tokens * 8);
@@ -475,13 +496,22 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             for (int j = 0; j < QL; ++j)
                 if (r < p.qrows && lane * 16 + j * 1024 < QB)
                     *reinterpret_cast<uint4*>(q_lds_b + (r * wpg + wi) * QB + lane * 16 + j * 1024) = qv[r][j];
-        if (tid <= rows) prefix[tid] = pv0;
-        if (tid + bd <= rows) prefix[tid + bd] = pv1;
-        if (tid < p.num_tokens) tok[tid] = make_int2(static_cast<int>(tv0[0]), static_cast<int>(tv0[1]));
-        if (tid + bd < p.num_tokens) tok[tid + bd] = make_int2(static_cast<int>(tv1[0]), static_cast<int>(tv1[1]));
-        for (int i = tid + 2 * bd; i <= rows; i += bd) prefix[i] = p.prefix_out[i];
-        for (int t = tid + 2 * bd; t < p.num_tokens; t += bd) tok[t] = p.plan_tok[t];
-        __syncthreads();
+        if (win) {
+            // Every wave writes the whole window, the same values at the same places, and reads only
+            // inside it after its own writes (LDS operations of a wave complete in order): no barrier.
+            if (lane <= kPlanWin) prefix[min(plan_rs + lane, rows)] = wpre;
+            if (lane == 0) prefix[rows] = wU;
+            if (lane < kPlanWin)
+                tok[min(plan_rs / hg_count + lane, p.num_tokens - 1)] = make_int2(wtkl, wtsq);
+        } else {
+            if (tid <= rows) prefix[tid] = pv0;
+            if (tid + bd <= rows) prefix[tid + bd] = pv1;
+            if (tid < p.num_tokens) tok[tid] = make_int2(static_cast<int>(tv0[0]), static_cast<int>(tv0[1]));
+            if (tid + bd < p.num_tokens) tok[tid + bd] = make_int2(static_cast<int>(tv1[0]), static_cast<int>(tv1[1]));
+            for (int i = tid + 2 * bd; i <= rows; i += bd) prefix[i] = p.prefix_out[i];
+            for (int t = tid + 2 * bd; t < p.num_tokens; t += bd) tok[t] = p.plan_tok[t];
+            __syncthreads();
+        }
     } else {
         build_row_prefix(p, rows, hg_count, prefix, tok);
         if (blockIdx.x == 0)
@@ -861,6 +891,16 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* pla
         rec.row = -1;
         rec.r_s = r_s;
         rec.r_e = end_row(pf, rows, u0, u1, r_s);
+        rec.U = static_cast<int>(U);
+        // the empty-row pass of the last workgroup may walk trailing empty rows up to `rows`
+        rec.win = rec.r_e - r_s <= kPlanWin - 1 && (w != G - 1 || rows - r_s <= kPlanWin - 1);
+        for (int i = 0; i <= kPlanWin; ++i) rec.pre[i] = prefix[min(r_s + i, rows)];
+        const int t_s = r_s / hg_count;
+        for (int j = 0; j < kPlanWin; ++j) {
+            const int t = min(t_s + j, p.num_tokens - 1);
+            rec.tkl[j] = tok[t].x;
+            rec.tsq[j] = tok[t].y;
+        }
         for (int r = r_s; r < rlim; ++r) {
             const int64_t pr0 = prefix[r], pr1 = prefix[r + 1];
             if (pr0 >= u1) break;
