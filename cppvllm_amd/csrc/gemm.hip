@@ -582,9 +582,6 @@ const GemmCfg* find_cfg(int code) {
         if (c.code() == code) return &c;
     return nullptr;
 }
-const GemmCfg* find_cfg(int mf, int nwn) {
-    return find_cfg(10 * mf + nwn + (nwn > 1 ? 100 : 0));
-}
 
 // Automatic choice. For the Qwen3-0.6B decode projections the configuration is the fastest one
 // measured on MI355X (HIP-graph replay, weights cold in the last-level cache) for the largest

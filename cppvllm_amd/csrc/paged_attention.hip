@@ -210,7 +210,8 @@ struct Params {
     const int64_t* token_seq;
     const int64_t* token_kv_len;
     int num_tokens;
-    int n_kv;
+    int n_kv;                // kv heads as the kernel sees them (virtual: physical << kv_shift)
+    int kv_shift;            // log2 of the virtual kv heads per physical kv head
     int wpg;                 // kv heads (waves) per workgroup
     int qrows;               // rows per workgroup whose q is staged in LDS by the prologue
     int log2_bs;
@@ -346,7 +347,9 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const int wi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = p.n_kv * REP;
     const int log2_bs = p.log2_bs;
-    const uint32_t row_bytes = static_cast<uint32_t>(p.n_kv) * HD;   // bytes of one slot (all kv heads)
+    const int kv_shift = p.kv_shift;
+    const int n_kv_phys = p.n_kv >> kv_shift;
+    const uint32_t row_bytes = static_cast<uint32_t>(n_kv_phys) * HD;   // bytes of one slot (all kv heads)
     const int64_t blk_bytes = static_cast<int64_t>(row_bytes) << log2_bs;
     const uint32_t blk_bytes32 = static_cast<uint32_t>(blk_bytes);
     const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
@@ -392,7 +395,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         const int p0 = tile * kTileKeys;
         const uint32_t lv = static_cast<uint32_t>(live);             // arithmetic, not a branch
         const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
-        const uint32_t lane_col = pc.g * HD + sub * E;              // byte column inside a slot row
+        const uint32_t lane_col = (pc.g >> kv_shift) * HD + sub * E;   // byte column inside a slot row
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
             const int64_t ph = (ONE_BLOCK || s < kSteps / 2) ? ph2.lo : ph2.hi;
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             tl.k[s] = buf_load<VT, POL>(make_rsrc(p.k_cache + ph * blk_bytes, kv_rec), off);
             tl.v[s] = buf_load<VT, POL>(make_rsrc(p.v_cache + ph * blk_bytes, kv_rec), off);
             if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
-                const int64_t sbase = (ph * p.n_kv + pc.g) << log2_bs;
+                const int64_t sbase = (ph * n_kv_phys + (pc.g >> kv_shift)) << log2_bs;
                 tl.ks[s] = buf_load_f32(make_rsrc(p.k_scale + sbase, s_rec), in_blk * 4u);
                 tl.vs[s] = buf_load_f32(make_rsrc(p.v_scale + sbase, s_rec), in_blk * 4u);
             } else {
@@ -1009,8 +1012,6 @@ bool launch_decode_rep(int rep, int G, int threads, size_t lds, hipStream_t s, c
     switch (rep) {
         case 1: launch_decode<HD, 1, SM>(G, threads, lds, s, p, one_block, planned); return true;
         case 2: launch_decode<HD, 2, SM>(G, threads, lds, s, p, one_block, planned); return true;
-        case 4: launch_decode<HD, 4, SM>(G, threads, lds, s, p, one_block, planned); return true;
-        case 8: launch_decode<HD, 8, SM>(G, threads, lds, s, p, one_block, planned); return true;
         default: return false;
     }
 }
@@ -1030,6 +1031,14 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (n_heads % n_kv_heads != 0) return CVH_ERR_UNSUPPORTED;
     const int rep = n_heads / n_kv_heads;
     if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return CVH_ERR_UNSUPPORTED;
+    // GQA 4 and 8: each kv head is presented to the kernel as rep/2 virtual kv heads of 2 query heads
+    // that read the same K/V (consecutive, so in one workgroup, reading each tile together: the
+    // second read hits the cache). One wave then holds two query heads' accumulators, as at GQA 2,
+    // instead of spilling 4 or 8 heads' worth of registers.
+    const int kv_split = rep > 2 ? rep / 2 : 1;
+    const int kv_shift = kv_split == 4 ? 2 : kv_split == 2 ? 1 : 0;
+    n_kv_heads *= kv_split;
+    const int rep_v = rep / kv_split;
     const int lg = ilog2_pow2(block_size);
     if (lg < 4 || lg > 12) return CVH_ERR_UNSUPPORTED;
     if (head_dim != 64 && head_dim != 128) return CVH_ERR_UNSUPPORTED;
@@ -1066,8 +1075,9 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     p.token_kv_len = token_kv_len;
     p.num_tokens = static_cast<int>(num_tokens);
     p.n_kv = n_kv_heads;
+    p.kv_shift = kv_shift;
     p.wpg = wpg;
-    p.qrows = q_stage_rows(wpg, rep, head_dim);
+    p.qrows = q_stage_rows(wpg, rep_v, head_dim);
     p.log2_bs = lg;
     // The softmax scale is folded into q with log2(e) (base-2 softmax); a per-tensor K scale is a
     // device float, so the kernel folds it into q after reading it.
@@ -1086,38 +1096,38 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (phase & kPhaseDecode) {
         const int planned = (phase & kPhasePlanned) ? ((phase & kPhaseShared) ? 2 : 1) : 0;
         const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens)) +
-                           static_cast<size_t>(p.qrows) * wpg * rep * head_dim * 2;
+                           static_cast<size_t>(p.qrows) * wpg * rep_v * head_dim * 2;
         const bool one_block = (1 << lg) >= kTileKeys;
         bool ok;
         if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
             ok = head_dim == 128
-                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block, planned)
-                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep, G, 64 * wpg, lds, s, p, one_block, planned);
+                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned)
+                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned);
         else
-            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block, planned)
-                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep, G, 64 * wpg, lds, s, p, one_block, planned);
+            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned)
+                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned);
         if (!ok) return CVH_ERR_UNSUPPORTED;
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
     if ((phase & kPhaseMerge) && G > 1) {
         const dim3 mgrid(static_cast<unsigned>(rows));
         // one thread per 4 output dims of the row's wpg*rep heads, up to 512 (more heads loop)
-        const int mthreads = std::min(512, wpg * rep * head_dim / 4);
+        const int mthreads = std::min(512, wpg * rep_v * head_dim / 4);
         const int nt = static_cast<int>(num_tokens);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
             else
                 paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, mthreads, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
         } else {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
             else
                 paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, mthreads, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
         }
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
@@ -1138,8 +1148,10 @@ extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_
     if (num_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0 ||
         partitions < 0 || n_heads % n_kv_heads != 0)
         return 0;
-    const int G = partitions ? partitions : cvh::auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
-    return cvh::ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G).total;
+    const int rep = n_heads / n_kv_heads;
+    const int n_kv = n_kv_heads * (rep > 2 ? rep / 2 : 1);   // the kernel's (virtual) kv heads, as in the launch
+    const int G = partitions ? partitions : cvh::auto_partitions(num_tokens, n_kv, table_width, block_size);
+    return cvh::ws_layout(num_tokens, n_heads, n_kv, head_dim, G).total;
 }
 
 #define CVH_PA_ARGS                                                                                                  \

@@ -58,8 +58,9 @@ enum { CVH_DTYPE_BF16 = 0, CVH_DTYPE_F16 = 1, CVH_DTYPE_F32 = 2 };
  *   token_kv_len int64 [num_tokens]  causal context length of each query token (positions+1);
  *                                    a token with kv_len <= 0 gets an all-zero output row
  *   scale        softmax scale (1/sqrt(head_dim) in the reference)
- * Supported: head_dim in {64,128}; n_heads/n_kv_heads in {1,2,4,8}; block_size a power of two
- * in [16, 4096]; num_tokens <= 8192 for n_kv_heads <= 8
+ * Supported: head_dim in {64,128}; n_heads/n_kv_heads in {1,2,4,8} (4 and 8 run as 2 and 4
+ * virtual kv heads of 2 query heads per kv head, which halves / quarters the token limit below);
+ * block_size a power of two in [16, 4096]; num_tokens <= 8192 for n_kv_heads <= 8
  * (num_tokens * n_kv_heads / 8 <= 8192 above): twice the reference engine's max_num_batched_tokens
  * (bench.cpp:25).
  * Queries of one sequence may be several tokens (chunked-prefill continuation).

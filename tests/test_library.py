@@ -121,10 +121,17 @@ def test_partition_policy_and_workspace_sizes():
     assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 256
     rows, slots = 256, 256 * 2 * 16     # [G][2][WPG*REP] partial slots
     r256 = lambda v: (v + 255) // 256 * 256
-    # plan: int2 token metadata [T] + int32 shared-prefix keys [T] + 64-byte workgroup records [G]
+    # plan: int2 token metadata [T] + int32 shared-prefix keys [T] + 184-byte workgroup records [G]
+    # (first piece and tiles, row range, row window of 9 prefix entries and 8 token records)
     want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4) + r256(256 * 8) + r256(256 * 4) + \
-        r256(256 * 64)
+        r256(256 * 184)
     assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == want
+    # GQA 4 / 8 run as 2 / 4 virtual kv heads of 2 query heads per kv head: twice / four times the rows
+    # (prefix), the same partial slots per query head
+    for H, vrows in ((32, 512), (64, 1024)):
+        want_v = r256((vrows + 1) * 4) + r256(256 * 2 * H // (vrows // 256) * 128 * 4) + \
+            r256(256 * 2 * H // (vrows // 256) * 2 * 4) + r256(256 * 8) + r256(256 * 4) + r256(256 * 184)
+        assert lib.cvh_paged_attention_workspace_bytes(256, H, 8, 128, 8, 256, 0) == want_v, H
     # small batches: never less than two tiles per partition
     assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
     assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 8 * 32 // 2
