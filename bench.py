@@ -71,7 +71,7 @@ def cpu_baseline(b, reps: int = 5):
         if i:
             times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    nbytes = workloads.attention_bytes(args[7].tolist())
+    nbytes = workloads.attention_bytes(args[7].tolist(), n_kv=KV, n_heads=H)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"one layer of config 3 (all 256 tokens, {nbytes / 1e6:.1f} MB algorithmic), "
                       f"median of {reps} after 1 warm-up: {med * 1e3:.1f} ms/layer"}
@@ -394,6 +394,8 @@ def main():
     ap.add_argument("--seqs", type=int, default=256,
                     help="config 3 with this many sequences (a smaller decode batch; the headline is 256)")
     ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
+    ap.add_argument("--tp", type=int, default=1, choices=(1, 2, 4, 8),
+                    help="configs 3/4 at one GPU's tensor-parallel share: kv heads 8/tp, query heads 16/tp")
     ap.add_argument("--no-shared-reuse", action="store_true",
                     help="config 4b without telling the plan which blocks are shared (all reads non-temporal)")
     ap.add_argument("--e2e", action="store_true", help="config 5: end-to-end generation tok/s through the engine")
@@ -444,6 +446,8 @@ def main():
         b = workloads.config3(device=dev, seqs=args.seqs)
     else:
         b = workloads.config4(device=dev, shared_prefix=args.shared_prefix)
+    if args.tp > 1:
+        b = workloads.tp_share(b, args.tp)
     lens = b["token_kv_len"].cpu().tolist()
     T, H, KV, HD, BS = len(lens), b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
     W = b["block_tables"].shape[1]
@@ -536,11 +540,12 @@ def main():
     dec_ms = timed(run_decode, args.steps)
     avg_layer_ms = dec_ms / (args.steps * len(layer_ptrs))
 
-    bytes_layer = workloads.attention_bytes(lens)
+    bytes_layer = workloads.attention_bytes(lens, n_kv=KV, n_heads=H)
     bytes_step = bytes_layer * len(layer_ptrs)
     value = bytes_step * args.steps / (total_ms / 1e3) / 1e9
     achieved = bytes_layer / (avg_layer_ms / 1e3) / 1e9
-    traffic = read_traffic() if args.config == 3 else None     # the PMC summary covers config 3
+    # the PMC summary covers config 3 at all 8 kv heads
+    traffic = read_traffic() if args.config == 3 and args.tp == 1 and args.seqs == 256 else None
     res = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -559,6 +564,8 @@ def main():
                          if args.config == 3 else
                          "BASELINE config 4%s: 64-seq long-context FP8 paged decode, 28 layers, distinct per-layer "
                          "caches" % ("b (shared 8-block prefix)" if args.shared_prefix else "")),
+            "tp_share": ("kv heads 0..%d of 8 (the first GPU's shard at tp=%d)" % (KV - 1, args.tp)) if args.tp > 1
+            else None,
             "seqs": T, "ctx_sum": int(sum(lens)), "ctx_min": int(min(lens)), "ctx_max": int(max(lens)),
             "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "block_size": BS, "layers": len(layer_ptrs),
             "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, KV, W, BS)

@@ -949,10 +949,14 @@ int64_t tile_bound(int64_t T, int n_kv, int64_t table_width, int block_size) {
     return T * (n_kv / waves_per_group(n_kv)) * per_row;
 }
 
+constexpr int kMaxAutoPartitions = 1024;
 int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
-    // one partition per resident workgroup slot, but never less than 2 tiles per partition
+    // one partition per resident workgroup slot, but never less than 2 tiles per partition and
+    // at most kMaxAutoPartitions workgroups: with one kv head (one-wave workgroups, a tp = 8
+    // share of config 3) 2048 partitions ran 21.3 us + a 30.6 us op, 1024 ran 18.9 / 24.9 us
     const int64_t b = (tile_bound(T, n_kv, table_width, block_size) + 1) / 2;
-    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kResidentWaves / waves_per_group(n_kv), b)));
+    const int64_t slots = std::min(kResidentWaves / waves_per_group(n_kv), kMaxAutoPartitions);
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots, b)));
 }
 
 // Workspace: prefix int32 [rows + 1] | part_acc float [G][2][WPG][REP][HD] | part_ml float2 [...]

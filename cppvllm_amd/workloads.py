@@ -129,6 +129,23 @@ def decode_batch(ctx_lens: list[int], bs: int, seed: int, device="cpu", per_tens
     }
 
 
+def tp_share(b: dict, tp: int) -> dict:
+    """The first GPU's shard of a decode batch under tensor parallelism over kv heads (the
+    reference's scaffold divides n_heads and n_kv_heads by tp, model_architecture.cpp:59-62):
+    kv heads [0, KV/tp) of the caches and scales and their query heads [0, H/tp); tables,
+    contexts and block pool unchanged."""
+    kv, h = b["n_kv_heads"] // tp, b["n_heads"] // tp
+    out = dict(b)
+    out["k_cache"] = b["k_cache"][:, :, :kv].contiguous()
+    out["v_cache"] = b["v_cache"][:, :, :kv].contiguous()
+    if b["k_scale"].dim() == 3:
+        out["k_scale"] = b["k_scale"][:, :kv].contiguous()
+        out["v_scale"] = b["v_scale"][:, :kv].contiguous()
+    out["q"] = b["q"][:, :h].contiguous()
+    out["n_kv_heads"], out["n_heads"] = kv, h
+    return out
+
+
 def config1_lens(seed: int = 1001, S: int = 8) -> list[int]:
     g = _cpu_gen(seed)
     return torch.randint(100, 1025, (S,), generator=g).tolist()

@@ -404,3 +404,20 @@ def test_shared_prefix_plan_is_bitwise_identical(orc):
     rows = [0, 1, 2, 3, 62, 63]
     assert_close_bf16(outs[1][rows], run_oracle(orc, {k: (v.cpu() if isinstance(v, torch.Tensor) else v)
                                                      for k, v in b.items()}, rows=rows))
+
+
+@pytest.mark.parametrize("tp", [2, 4, 8])
+def test_tp_share_matches_full_heads(orc, tp):
+    """One GPU's tensor-parallel shard of config 3 (kv heads [0, 8/tp), their query heads, the
+    real contexts) gives the same output as those heads of the full 8-kv-head launch (within the
+    tolerance: the work partition, and so the summation order, depends on the head count), and
+    matches the oracle on a sample of its rows."""
+    say(f"tp share {tp} of config 3 (64 sequences)")
+    b = workloads.config3(device=DEV, seqs=64)
+    full = run_gpu(b)
+    s = workloads.tp_share(b, tp)
+    shard = run_gpu(s)
+    h = s["n_heads"]
+    assert_close_bf16(shard, full[:, :h])
+    rows = np.arange(0, 64, 9)
+    assert_close_bf16(shard[rows], run_oracle(orc, s, rows))

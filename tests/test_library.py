@@ -135,6 +135,9 @@ def test_partition_policy_and_workspace_sizes():
     # small batches: never less than two tiles per partition
     assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
     assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 8 * 32 // 2
+    # one kv head: one-wave workgroups, capped at 1024 (not one per resident wave slot, 2048)
+    assert lib.cvh_paged_attention_partitions(256, 1, 8, 256) == 1024
+    assert lib.cvh_paged_attention_partitions(256, 2, 8, 256) == 1024
     assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 8, 16, -1) == 0
 
 
