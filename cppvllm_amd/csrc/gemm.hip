@@ -349,10 +349,15 @@ __global__ __launch_bounds__(256) void gemm_oneshot_kernel(uint16_t* __restrict_
 // The DMA is issued from inline assembly on purpose: the compiler cannot tell which LDS stage a
 // global_load_lds writes and would wait for all of them (vmcnt(0)) before any LDS read, which
 // serialises the ring. The kernel therefore counts vmcnt itself; it issues no other vector-memory
-// loads, so the compiler's own counter bookkeeping is unaffected.
+// loads, so the compiler's own counter bookkeeping is unaffected. M0 (the LDS destination) is
+// saved and restored inside the statement: the compiler does not honour M0 as a clobber.
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr)
-                 : "memory", "m0");
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(gptr), "s"(lds_addr)
+                 : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
