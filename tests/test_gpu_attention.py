@@ -320,6 +320,51 @@ def test_plan_shared_by_layers_config3(orc):
     assert_close_bf16(got1[rows], run_oracle(orc, cpu, rows=rows))
 
 
+def test_planned_repeated_graph_launches():
+    """One plan, 28 planned launches alternating two different caches in a HIP graph, replayed
+    with eager work in between: every output equals the unplanned call bitwise, so no launch
+    reads another launch's partials or plan state."""
+    say("planned: 28 launches x 4 graph replays, alternating caches")
+    b = workloads.config3(device=DEV, seqs=128)
+    T, H, HD = b["q"].shape
+    KV, BS, W = b["n_kv_heads"], b["block_size"], b["block_tables"].shape[1]
+    b2 = dict(b)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    b2["k_cache"] = torch.randint(0, 126, b["k_cache"].shape, dtype=torch.uint8, device=DEV, generator=g)
+    b2["v_cache"] = torch.randint(0, 126, b["v_cache"].shape, dtype=torch.uint8, device=DEV, generator=g)
+    want = [run_gpu(b), run_gpu(b2)]
+    assert not np.array_equal(want[0], want[1])
+    ws = ops.paged_attention_workspace(T, H, KV, HD, W, BS, 0, DEV)
+    ops.paged_attention_plan(b["block_tables"], b["token_seq"], b["token_kv_len"], H, KV, HD, BS, ws)
+    outs = [torch.empty_like(b["q"]) for _ in range(28)]
+
+    def layers():
+        for i, o in enumerate(outs):
+            c = b if i % 2 == 0 else b2
+            ops.paged_attention_fp8(o, c["q"], c["k_cache"], c["v_cache"], c["k_scale"], c["v_scale"],
+                                    c["block_tables"], c["token_seq"], c["token_kv_len"], c["scale"], workspace=ws,
+                                    planned=True)
+    layers()
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert np.array_equal(bits(o), want[i % 2]), f"eager launch {i}"
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            layers()
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            assert np.array_equal(bits(o), want[i % 2]), f"replay {rep} launch {i}"
+        assert np.array_equal(run_gpu(b2), want[1])          # eager work between replays
+
+
 # ---- the MFMA multi-query (chunked-prefill) kernel -------------------------------------------------
 def synth_prefill(seed, chunks, BS, H=16, KV=8, per_tensor=False, order="asc"):
     """chunks: (context length L, query tokens n) per sequence -> the n last positions of each
