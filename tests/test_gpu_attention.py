@@ -4,14 +4,15 @@ Bar: max-abs 2e-2 and mean-abs 2e-3 on the bf16 outputs (the build's stated tole
 Covers BASELINE configs 1 (both scale modes), 3 (full headline size), 4 and 4b (long contexts,
 split-K, shared prefix blocks, outliers), the reference's 16-token blocks, GQA ratios 1/2/4/8,
 head_dim 64, ragged and boundary lengths, chunked-prefill continuation rows, empty contexts,
-split-count invariance and physical-block permutation invariance."""
+split-count invariance and physical-block permutation invariance, block sizes 16 to 4096 and the
+query-token limits of the GQA 4/8 virtual kv heads."""
 import math
 
 import numpy as np
 import pytest
 import torch
 
-from cppvllm_amd import ops, workloads
+from cppvllm_amd import _lib, ops, workloads
 from tests._util import assert_close_bf16, bits, np_, say
 
 pytestmark = pytest.mark.gpu
@@ -87,6 +88,7 @@ def test_config1(orc, per_tensor):
 @pytest.mark.parametrize("BS,H,KV,HD,per_tensor", [
     (16, 16, 8, 128, False), (16, 16, 8, 128, True), (256, 16, 8, 128, False), (32, 8, 8, 128, False),
     (64, 32, 8, 128, False), (16, 64, 8, 128, False), (16, 8, 2, 64, False), (128, 16, 4, 64, True),
+    (4096, 16, 8, 128, False), (1024, 32, 8, 128, False), (512, 64, 8, 64, True), (2048, 8, 8, 128, False),
 ])
 def test_shapes_and_boundaries(orc, BS, H, KV, HD, per_tensor):
     lens = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 255, 256, 257, 511, 777, 1030]
@@ -123,6 +125,25 @@ def test_max_rows_per_launch(orc):
     got = run_gpu(dev(b))
     rows = sorted(np.random.default_rng(41).choice(8192, 192, replace=False).tolist())
     assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
+
+
+@pytest.mark.parametrize("H,limit", [(32, 4096), (64, 2048)])
+def test_virtual_head_row_limits(orc, H, limit):
+    """GQA 4 / 8 run as 2 / 4 virtual kv heads per kv head, so at 8 kv heads a launch takes at
+    most 4096 / 2048 query tokens: the limit itself is computed (sampled rows vs the oracle), one
+    token more is rejected with CVH_ERR_UNSUPPORTED before anything runs."""
+    say(f"virtual-head row limit H={H} T={limit}")
+    per = limit // 4
+    b = synth(43 + H, [per + 50, per + 300, per + 7, per + 999], 256, H=H, queries_per_seq=per)
+    assert b["q"].shape[0] == limit
+    got = run_gpu(dev(b))
+    rows = sorted(np.random.default_rng(H).choice(limit, 96, replace=False).tolist())
+    assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
+    b1 = dev(synth(44 + H, [per + 50, per + 300, per + 7, per + 999], 256, H=H, queries_per_seq=per + 1))
+    assert b1["q"].shape[0] == limit + 4
+    with pytest.raises(_lib.CvhError) as err:
+        run_gpu(b1)
+    assert err.value.code == _lib.CVH_ERR_UNSUPPORTED
 
 
 def test_empty_context_rows_are_zero(orc):
