@@ -685,46 +685,77 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     };
     // End of a piece: combine the 8 key groups (rescale each to the wave max, then sum) and
     // write the finished row, or the partial of a cut row to slot 0 (holds u0) / 1 (holds u1-1).
+    // The 8 key groups are combined by a reduce-scatter: each lane starts with REP*E partial
+    // values (REP heads x E dims) and ends with NV/8 of them summed over the 8 groups, so every
+    // lane converts and stores NV/8 consecutive dims of one head instead of group 0 handling all.
+    // Levels: xor 16 and xor 32 with the permlane swaps (one swap exchanges a pair of halves:
+    // swap(vdst = upper, src = lower) leaves even rows / lower lanes the two upper halves and the
+    // others the two lower halves, so one add finishes the pair), then xor 8 with DPP.
+    constexpr int NV = REP * E, NV8 = NV / 8;
+    static_assert(NV8 >= 1 && E % NV8 == 0, "each lane's share lies in one head");
+    const int b3 = (lane >> 3) & 1, b4 = (lane >> 4) & 1, b5 = (lane >> 5) & 1;
+    const int v_own = (b4 ? 0 : NV / 2) + (b5 ? 0 : NV / 4) + (b3 ? NV8 : 0);   // first value index kept
+    const int r_own = v_own / E, e_own = v_own % E;
     auto finish = [&](const Piece& pc) {
+        float cs[REP];
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
             const float M = across_groups_max(m[r]);
-            const float c = __builtin_amdgcn_exp2f(m[r] - M);
+            cs[r] = __builtin_amdgcn_exp2f(m[r] - M);
             m[r] = M;
-            l[r] = across_groups_sum(l[r] * c);   // l is uniform inside a group
-#pragma unroll
-            for (int e = 0; e < E; ++e) acc[r][e] = across_groups_sum(acc[r][e] * c);
+            l[r] = across_groups_sum(l[r] * cs[r]);   // l is uniform inside a group
         }
-        if (grp != 0) return;
+        float a16[NV / 2];
+#pragma unroll
+        for (int i = 0; i < NV / 2; ++i) {
+            const float lo = acc[i / E][i % E] * cs[i / E];
+            const float hi = acc[(NV / 2 + i) / E][(NV / 2 + i) % E] * cs[(NV / 2 + i) / E];
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(hi), __float_as_uint(lo), false, false);
+            a16[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        float a32[NV / 4];
+#pragma unroll
+        for (int i = 0; i < NV / 4; ++i) {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(a16[NV / 4 + i]), __float_as_uint(a16[i]),
+                                                             false, false);
+            a32[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        float res[NV8];
+#pragma unroll
+        for (int i = 0; i < NV8; ++i) {
+            const float x = a32[i], y = a32[NV8 + i];
+            const float keep = b3 ? y : x, send = b3 ? x : y;
+            res[i] = keep + dpp_xor8(send);
+        }
+        float l_own = l[0], m_own = m[0];
+#pragma unroll
+        for (int r = 1; r < REP; ++r)
+            if (r_own == r) {
+                l_own = l[r];
+                m_own = m[r];
+            }
         const int64_t pr0 = pfx(pc.row), pr1 = pfx(pc.row + 1);
         if (pc.lt == 0 && pc.le == pr1 - pr0) {
             const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
+            const float f = vfin / l_own;
+            uint16_t* o = p.out + ((int64_t)pc.t * H + pc.g * REP + r_own) * HD + sub * E + e_own;
+            if constexpr (NV8 == 1) {
+                *o = f32_to_bf16_bits(res[0] * f);
+            } else {
+                uint32_t wd[NV8 / 2];
 #pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                const float f = vfin / l[r];
-                uint16_t* o = p.out + ((int64_t)pc.t * H + pc.g * REP + r) * HD + sub * E;
-#pragma unroll
-                for (int c = 0; c < E / 8; ++c) {
-                    uint32_t wd[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        wd[i] = f32_to_bf16_bits(acc[r][c * 8 + 2 * i] * f) |
-                                (uint32_t(f32_to_bf16_bits(acc[r][c * 8 + 2 * i + 1] * f)) << 16);
-                    reinterpret_cast<uint4*>(o)[c] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-                }
+                for (int i = 0; i < NV8 / 2; ++i)
+                    wd[i] = f32_to_bf16_bits(res[2 * i] * f) | (uint32_t(f32_to_bf16_bits(res[2 * i + 1] * f)) << 16);
+                if constexpr (NV8 == 4) *reinterpret_cast<uint2*>(o) = make_uint2(wd[0], wd[1]);
+                else *reinterpret_cast<uint32_t*>(o) = wd[0];
             }
         } else {
             const int slot = (pr0 <= u0) ? 0 : 1;
+            const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP + r_own;
+            float* pa = p.part_acc + idx * HD + sub * E + e_own;
 #pragma unroll
-            for (int r = 0; r < REP; ++r) {
-                const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP + r;
-                float* pa = p.part_acc + idx * HD + sub * E;
-#pragma unroll
-                for (int c = 0; c < E / 4; ++c)
-                    reinterpret_cast<float4*>(pa)[c] =
-                            make_float4(acc[r][4 * c], acc[r][4 * c + 1], acc[r][4 * c + 2], acc[r][4 * c + 3]);
-                if (sub == 0) reinterpret_cast<float2*>(p.part_ml)[idx] = make_float2(m[r], l[r]);
-            }
+            for (int i = 0; i < NV8; ++i) pa[i] = res[i];
+            if (sub == 0 && e_own == 0) reinterpret_cast<float2*>(p.part_ml)[idx] = make_float2(m_own, l_own);
         }
     };
 
