@@ -335,6 +335,27 @@ def test_attention_oracle_vs_float64(orc, BS, HD, REP, per_tensor):
     assert (err <= np.abs(want) * 2.0 ** -8 * 1.01 + 1e-7).mean() > 0.97
 
 
+@pytest.mark.parametrize("tp", [2, 4, 8])
+def test_tp_share_slices_heads(orc, tp):
+    """workloads.tp_share (one GPU's shard under tensor parallelism over kv heads) keeps kv heads
+    [0, 8/tp) of caches and scales and their query heads: the oracle on the shard equals the first
+    16/tp heads of the oracle on the full batch, bit for bit (each (token, head) is computed
+    independently)."""
+    from cppvllm_amd import workloads
+    b = workloads.decode_batch([40, 300, 17, 520], 16, 77)
+    s = workloads.tp_share(b, tp)
+    H, KV = b["n_heads"], b["n_kv_heads"]
+    assert (s["n_heads"], s["n_kv_heads"]) == (H // tp, KV // tp)
+    assert s["k_cache"].shape == (b["num_blocks"], 16, KV // tp, 128) and s["k_cache"].is_contiguous()
+
+    def run(d):
+        host = [d[k].numpy() if d[k].dtype != torch.bfloat16 else d[k].view(torch.int16).numpy().view(np.uint16)
+                for k in ("q", "k_cache", "v_cache", "k_scale", "v_scale", "block_tables", "token_seq", "token_kv_len")]
+        return orc.paged_attention_fp8(*host, d["n_heads"], d["n_kv_heads"], 128, 16, orc.PER_TOKEN_HEAD, d["scale"])
+    full, shard = run(b), run(s)
+    assert np.array_equal(shard, full[:, :H // tp])
+
+
 def test_attention_known_answers(orc):
     rng = np.random.default_rng(1)
     H, KV, HD, BS = 2, 1, 128, 16
