@@ -98,6 +98,49 @@ struct AgentChunk {
     }
 };
 
+// ---- DPP helpers (within rows of 16 lanes) ---------------------------------------------------
+// All patterns below give every lane a valid source lane, so bound_ctrl (zero for invalid
+// sources) never applies; setting it lets the compiler fold the move into the consuming VALU op
+// (v_add_f32_dpp / v_max_f32_dpp).
+template <int CTRL> __device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// lane ^ 1 and lane ^ 2 inside a quad (quad_perm [1,0,3,2] and [2,3,0,1]).
+__device__ __forceinline__ float dpp_xor1(float v) { return dpp<0xB1>(v); }
+__device__ __forceinline__ float dpp_xor2(float v) { return dpp<0x4E>(v); }
+// row_half_mirror: lane i <-> 7-i inside each group of 8. After the xor1/xor2 levels a quad is
+// uniform, so this pairs quad 0 with quad 1 exactly like an xor-4 exchange would.
+__device__ __forceinline__ float dpp_half_mirror(float v) { return dpp<0x141>(v); }
+// row_mirror: lane i <-> 15-i inside each row of 16 (an xor-8 exchange once halves are uniform).
+__device__ __forceinline__ float dpp_mirror(float v) { return dpp<0x140>(v); }
+// row_ror:8: lane i <-> (i+8) mod 16 inside each row of 16, i.e. exactly lane ^ 8.
+__device__ __forceinline__ float dpp_xor8(float v) { return dpp<0x128>(v); }
+
+// The xor butterfly over aligned groups of N lanes (N = 16 or 64; every lane of a group active):
+// level m combines lane i with lane i ^ m for m = 1, 2, 4, ..., so the result equals the
+// __shfl_xor butterfly bit for bit, but with DPP (xor 4 and 8 as mirrors once quads / halves are
+// uniform) and the gfx950 permlane swaps for xor 16 / 32 instead of LDS-routed ds_bpermute.
+template <int N, typename Op> __device__ __forceinline__ float xor_butterfly(float v, Op op) {
+    static_assert(N == 16 || N == 64, "row or wave");
+    v = op(v, dpp_xor1(v));
+    v = op(v, dpp_xor2(v));
+    v = op(v, dpp_half_mirror(v));
+    v = op(v, dpp_mirror(v));
+    if constexpr (N == 64) {
+        auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+        r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    return v;
+}
+template <int N> __device__ __forceinline__ float xor_sum(float v) {
+    return xor_butterfly<N>(v, [](float a, float b) { return a + b; });
+}
+template <int N> __device__ __forceinline__ float xor_max(float v) {
+    return xor_butterfly<N>(v, [](float a, float b) { return fmaxf(a, b); });
+}
+
 // RMSNorm (ADD: after resid <- rnd(resid + x), normalising resid) of one row of `dim` elements
 // (dim % 8 == 0, dim <= 512 * MAXC) by the 64 lanes of a wave: lane l owns chunks l, l+64, ...;
 // the sum of squares runs over the lane's elements in index order, then an xor butterfly over the
@@ -140,8 +183,7 @@ __device__ __forceinline__ void norm_row(typename Elem<DT>::T* __restrict__ orow
             }
         }
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss = ss + __shfl_xor(ss, m, 64);
+    ss = xor_sum<64>(ss);
     const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(dim) + eps);
 #pragma unroll
     for (int j = 0; j < MAXC; ++j) {
@@ -203,24 +245,6 @@ __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
     f[2] = hi[0];
     f[3] = hi[1];
 }
-
-// ---- DPP helpers (within rows of 16 lanes) ---------------------------------------------------
-// All patterns below give every lane a valid source lane, so bound_ctrl (zero for invalid
-// sources) never applies; setting it lets the compiler fold the move into the consuming VALU op
-// (v_add_f32_dpp / v_max_f32_dpp).
-template <int CTRL> __device__ __forceinline__ float dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-// lane ^ 1 and lane ^ 2 inside a quad (quad_perm [1,0,3,2] and [2,3,0,1]).
-__device__ __forceinline__ float dpp_xor1(float v) { return dpp<0xB1>(v); }
-__device__ __forceinline__ float dpp_xor2(float v) { return dpp<0x4E>(v); }
-// row_half_mirror: lane i <-> 7-i inside each group of 8. After the xor1/xor2 levels a quad is
-// uniform, so this pairs quad 0 with quad 1 exactly like an xor-4 exchange would.
-__device__ __forceinline__ float dpp_half_mirror(float v) { return dpp<0x141>(v); }
-// row_mirror: lane i <-> 15-i inside each row of 16 (an xor-8 exchange once halves are uniform).
-__device__ __forceinline__ float dpp_mirror(float v) { return dpp<0x140>(v); }
-// row_ror:8: lane i <-> (i+8) mod 16 inside each row of 16, i.e. exactly lane ^ 8.
-__device__ __forceinline__ float dpp_xor8(float v) { return dpp<0x128>(v); }
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 

@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
         float amax = 0.f;
 #pragma unroll
         for (int j = 0; j < 2 * P; ++j) amax = fmaxf(amax, fabsf(x[j]));
-        for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+        amax = xor_max<16>(amax);
         if (v_dense != nullptr) {
             uint16_t* d = v_dense + (t * KV + kvh) * HD;
 #pragma unroll
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 2 * P; ++j) ss = ss + x[j] * x[j];
-    for (int m = 1; m < 16; m <<= 1) ss = ss + __shfl_xor(ss, m, 16);
+    ss = xor_sum<16>(ss);
     const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(HD) + eps);
 
     float n[2 * P];
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < 2 * P; ++j) { r[j] = round_bf16(r[j]); amax = fmaxf(amax, fabsf(r[j])); }
-    for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+    amax = xor_max<16>(amax);
     if (k_dense != nullptr) {
         uint16_t* d = k_dense + (t * KV + kvh) * HD;
 #pragma unroll
