@@ -31,7 +31,8 @@
 //   * q.k partial dots reduce over the 8 lanes of a key with DPP (quad_perm, half-mirror);
 //   * softmax in base 2 (scale*log2(e) folded into q) with a running max per key group and a
 //     lazy rescale (only when a tile's max exceeds the running max by 2^8), exact because l and
-//     acc share the stale max; groups are combined once per piece (DPP row_ror:8, permlane swaps).
+//     acc share the stale max; groups are combined once per piece by a reduce-scatter (permlane
+//     swaps, DPP row_ror:8), each lane ending with a few finished dims to convert and store.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
