@@ -28,6 +28,23 @@ def test_swiglu_bitexact(orc, T, I, dtype):
     assert np.array_equal(got, want)
 
 
+def test_swiglu_every_bf16_gate(orc):
+    """Every one of the 65536 bf16 gate values (NaN, infinities, subnormals included) gives the
+    oracle's result bit for bit, with u = 1 (silu itself) and with random u."""
+    say("swiglu over every bf16 gate value")
+    g_bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).reshape(64, 1024)
+    gen = torch.Generator().manual_seed(17)
+    for u in (torch.ones((64, 1024)).to(torch.bfloat16), (torch.randn((64, 1024), generator=gen) * 3).to(torch.bfloat16)):
+        gu = torch.cat([g_bits, u], dim=1)
+        out = torch.empty((64, 1024), dtype=torch.bfloat16, device=DEV)
+        ops.fused.swiglu(out, gu.to(DEV))
+        torch.cuda.synchronize()
+        want = orc.swiglu(np_(gu), dtype=orc.BF16)
+        got = np_(out)
+        bad = np.nonzero(got != want)
+        assert bad[0].size == 0, f"{bad[0].size} mismatches, first at {bad[0][0]},{bad[1][0]}"
+
+
 @pytest.mark.parametrize("ldtype", [torch.float32, torch.bfloat16])
 def test_greedy_sampler_full_vocab(orc, ldtype):
     say(f"greedy sampler R=256 V=151936 {ldtype}")
