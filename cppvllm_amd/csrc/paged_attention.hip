@@ -982,12 +982,17 @@ int64_t tile_bound(int64_t T, int n_kv, int64_t table_width, int block_size) {
 }
 
 constexpr int kMaxAutoPartitions = 1024;
+constexpr int64_t kMaxPiecesPerRow = 8;
 int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
     // one partition per resident workgroup slot, but never less than 2 tiles per partition and
     // at most kMaxAutoPartitions workgroups: with one kv head (one-wave workgroups, a tp = 8
     // share of config 3) 2048 partitions ran 21.3 us + a 30.6 us op, 1024 ran 18.9 / 24.9 us
+    // and at most kMaxPiecesPerRow partitions per row: a small batch cut finer only lengthens the
+    // merge of each row (16 sequences: 256 partitions op 30.5 us, 128 partitions 26.6 us)
     const int64_t b = (tile_bound(T, n_kv, table_width, block_size) + 1) / 2;
-    const int64_t slots = std::min(kResidentWaves / waves_per_group(n_kv), kMaxAutoPartitions);
+    const int64_t rows = T * (n_kv / waves_per_group(n_kv));
+    const int64_t slots = std::min({static_cast<int64_t>(kResidentWaves / waves_per_group(n_kv)),
+                                    static_cast<int64_t>(kMaxAutoPartitions), kMaxPiecesPerRow * rows});
     return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots, b)));
 }
 

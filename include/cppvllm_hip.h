@@ -76,8 +76,8 @@ int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* k_cache, co
 
 /* Same as cvh_paged_attention_fp8 with an explicit work partition count: the concatenated
  * 32-key tiles of all (token, kv-head group) rows are cut into `partitions` equal ranges, one
- * workgroup each; 0 = automatic (one per resident workgroup slot of an MI355X, at most 1024,
- * fewer for small batches). Results agree to fp32 rounding for every partition count.
+ * workgroup each; 0 = automatic (one per resident workgroup slot of an MI355X, at most 1024 and
+ * at most 8 per row, fewer for small batches). Results agree to fp32 rounding for every partition count.
  * (No reference counterpart for the knob: the reference hard-codes a split heuristic,
  *  kernels/paged_attention.cu:403-409; tests use it to prove partition invariance.) */
 int cvh_paged_attention_fp8_ex(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,

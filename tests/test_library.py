@@ -134,7 +134,9 @@ def test_partition_policy_and_workspace_sizes():
         assert lib.cvh_paged_attention_workspace_bytes(256, H, 8, 128, 8, 256, 0) == want_v, H
     # small batches: never less than two tiles per partition
     assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
-    assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 8 * 32 // 2
+    # few rows: at most 8 partitions per row (8 rows -> 64, though 2 tiles each would allow 128)
+    assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 64
+    assert lib.cvh_paged_attention_partitions(16, 8, 8, 256) == 128
     # one kv head: one-wave workgroups, capped at 1024 (not one per resident wave slot, 2048)
     assert lib.cvh_paged_attention_partitions(256, 1, 8, 256) == 1024
     assert lib.cvh_paged_attention_partitions(256, 2, 8, 256) == 1024
