@@ -894,6 +894,78 @@ __global__ __launch_bounds__(512) void paged_merge_kernel(uint16_t* __restrict__
     }
 }
 
+// Two halves of 512 threads per row (every thread one head slice, so the halves' loops agree in
+// length): half p folds pieces w0 + p, w0 + p + 2, ... online, then half 1 hands its (M, L, A)
+// to half 0 through LDS, which combines the two; a row's chain of dependent piece loads is half
+// as long (small batches cut a row into up to 8 pieces).
+template <int HD, int SM>
+__global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
+                                                          const float* __restrict__ part_ml,
+                                                          const int* __restrict__ prefix,
+                                                          const float* __restrict__ v_scale, int num_tokens, int n_kv,
+                                                          int rep, int wpg, int G) {
+    constexpr int TPH = HD / 4;                       // threads per query head
+    const int row = blockIdx.x;
+    const int hg_count = n_kv / wpg;
+    const int heads_per_row = wpg * rep;             // query heads of one row group
+    const int rows = num_tokens * hg_count;
+    const int64_t U = prefix[rows];
+    const int64_t pr0 = prefix[row], pr1 = prefix[row + 1];
+    if (pr1 == pr0) return;
+    // workgroup holding tile u: the largest w with w*U/G <= u
+    auto owner = [&](int64_t u) { return static_cast<int>(((u + 1) * G - 1) / U); };
+    const int w0 = owner(pr0), w1 = owner(pr1 - 1);
+    if (w0 == w1) return;
+    const int t = row / hg_count, hgi = row % hg_count;
+    const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
+    __shared__ float xs[6][512];
+    const int half = static_cast<int>(blockDim.x) / 2, part = static_cast<int>(threadIdx.x) >= half ? 1 : 0;
+    const int ti = static_cast<int>(threadIdx.x) - part * half;
+    {
+        const int hh = ti / TPH;
+        const int d0 = (ti % TPH) * 4;
+        float M = kMinusHuge, L = 0.f;
+        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+        for (int w = w0 + part; w <= w1; w += 2) {
+            // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
+            if (w * U / G == (w + 1) * U / G) continue;
+            const int slot = (pr0 <= w * U / G) ? 0 : 1;
+            const int64_t idx = (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh;
+            const float2 ml = reinterpret_cast<const float2*>(part_ml)[idx];
+            const float4 a = *reinterpret_cast<const float4*>(part_acc + idx * HD + d0);
+            const float Mn = fmaxf(M, ml.x);
+            const float co = exp2f(M - Mn), cn = exp2f(ml.x - Mn);
+            L = L * co + ml.y * cn;
+            A.x = A.x * co + a.x * cn;
+            A.y = A.y * co + a.y * cn;
+            A.z = A.z * co + a.z * cn;
+            A.w = A.w * co + a.w * cn;
+            M = Mn;
+        }
+        if (part) {
+            xs[0][ti] = M; xs[1][ti] = L; xs[2][ti] = A.x; xs[3][ti] = A.y; xs[4][ti] = A.z; xs[5][ti] = A.w;
+        }
+        __syncthreads();
+        if (part) return;
+        {
+            const float M1 = xs[0][ti], Mn = fmaxf(M, M1);
+            const float c0 = exp2f(M - Mn), c1 = exp2f(M1 - Mn);
+            L = L * c0 + xs[1][ti] * c1;
+            A.x = A.x * c0 + xs[2][ti] * c1;
+            A.y = A.y * c0 + xs[3][ti] * c1;
+            A.z = A.z * c0 + xs[4][ti] * c1;
+            A.w = A.w * c0 + xs[5][ti] * c1;
+        }
+        const float f = vfin / L;
+        const int h = hgi * heads_per_row + hh;      // query head index within the token
+        uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
+        const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
+        const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
+        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+    }
+}
+
 // Plan of a batch layout, built once and shared by every launch over the same block tables,
 // token_seq, token_kv_len and partition count (the 28 layers of a decode step): the row
 // prefix and token metadata the decode workgroups would derive, and each workgroup's first
@@ -1155,6 +1227,26 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         // one thread per 4 output dims of the row's wpg*rep heads, up to 512 (more heads loop)
         const int mthreads = std::min(512, wpg * rep_v * head_dim / 4);
         const int nt = static_cast<int>(num_tokens);
+        // every thread one head slice: two halves split the row's pieces
+        if (wpg * rep_v * head_dim / 4 <= 512) {
+            const int m2 = 2 * (wpg * rep_v * head_dim / 4);
+            if (head_dim == 128) {
+                if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
+                    paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
+                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+                else
+                    paged_merge2_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
+                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+            } else {
+                if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
+                    paged_merge2_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
+                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+                else
+                    paged_merge2_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
+                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+            }
+            return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+        }
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
