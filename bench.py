@@ -568,7 +568,7 @@ def main():
             else None,
             "seqs": T, "ctx_sum": int(sum(lens)), "ctx_min": int(min(lens)), "ctx_max": int(max(lens)),
             "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "block_size": BS, "layers": len(layer_ptrs),
-            "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, KV, W, BS)
+            "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, H, KV, W, BS)
             if args.partitions == 0 else args.partitions,
             "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "launch": "eager" if args.eager else "hip_graph",

@@ -51,7 +51,7 @@ SIGNATURES = {
     "cvh_paged_attention_fp8_planned_split_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32,
                                                           i32, i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_workspace_bytes": (sz, [i64, i32, i32, i32, i64, i32, i32]),
-    "cvh_paged_attention_partitions": (i32, [i64, i32, i64, i32]),
+    "cvh_paged_attention_partitions": (i32, [i64, i32, i32, i64, i32]),
     "cvh_rms_norm": (i32, [vp, vp, vp, i64, i32, f64, i32, vp]),
     "cvh_add_rms_norm": (i32, [vp, vp, vp, vp, i64, i32, f64, i32, vp]),
     "cvh_qk_norm_rope_kv_write_fp8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i32, i32,

@@ -12,7 +12,7 @@
 //   sampler: arg-max with the lowest index winning ties (kernels/fused_ops.cu:302-303); the
 //            Gumbel score of a sampling row is (float)(x*inv_t - log(max(-log(u), 1e-10))) in
 //            double, u from Philox-4x32-10 (Salmon et al., SC'11) with the counter layout of
-//            kernels/fused_ops.cu:327-330.
+//            kernels/fused_ops.cu:327-330 (index/4, row, offset).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -75,7 +75,20 @@ __global__ __launch_bounds__(256) void swiglu_scalar_kernel(typename Elem<DT>::T
 }
 
 // ---- Sampler ----------------------------------------------------------------------------------
-constexpr int kSampleThreads = 1024;   // 16 waves per row
+// Design: every candidate becomes one 64-bit key whose unsigned order is the selection order,
+//   key = order32(score) << 32 | (0xFFFFFFFF - index),
+// so "largest score, lowest index on ties" is a plain unsigned max and a row's winner is the max
+// over all its keys. order32 maps float bit patterns to an unsigned order (negatives bit-flipped,
+// positives with the sign bit set) and sends NaN below every number, so a NaN never wins. The
+// search starts from the key of (-inf, index 0x7FFFFFFF): an all -inf row then gives index 0 and
+// an all-NaN row 0x7FFFFFFF, as the reference's (value, index) scan does (kernels/fused_ops.cu:
+// 300-306).
+// Work split: one workgroup of kSampleWaves waves per row; wave w owns the contiguous slice
+// [w*S, (w+1)*S) of the vocab (S a multiple of 8), and its lanes read 8 logits (16 bytes of bf16)
+// at a time, lane-consecutive, so one load instruction of a wave covers 1 KB contiguous. Each
+// lane folds its keys with a 64-bit max; the wave folds them with a DPP/permlane butterfly on the
+// two 32-bit halves; wave leaders fold into one LDS word with ds_max_u64.
+constexpr int kSampleWaves = 16;
 
 // Philox-4x32 with 10 rounds (Random123's philox4x32_10): multipliers 0xD2511F53 / 0xCD9E8D57,
 // Weyl key increments 0x9E3779B9 / 0xBB67AE85.
@@ -94,105 +107,127 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
     }
 }
 
-struct Best {
-    float v;
-    int i;
-};
-__device__ __forceinline__ bool better(float v, int i, const Best& b) { return v > b.v || (v == b.v && i < b.i); }
+__device__ __forceinline__ uint64_t rank_key(float s, uint32_t index) {
+    const uint32_t b = __float_as_uint(s);
+    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    if ((b & 0x7fffffffu) > 0x7f800000u) o = 0u;   // NaN: below -inf
+    return (static_cast<uint64_t>(o) << 32) | (0xFFFFFFFFu - index);
+}
+__device__ __forceinline__ uint32_t key_index(uint64_t k) { return 0xFFFFFFFFu - static_cast<uint32_t>(k); }
+__device__ __forceinline__ uint64_t kmax(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-__device__ __forceinline__ float gumbel_score(float x, float inv_t, uint32_t r) {
-    const float u = (static_cast<float>(r >> 8) + 0.5f) * (1.0f / 16777216.0f);   // exact
-    const double e = fmax(-log(static_cast<double>(u)), 1e-10);
-    return static_cast<float>(static_cast<double>(x) * inv_t - log(e));
+// Gumbel perturbation of logit x with the 32-bit uniform word r: u = ((r >> 8) + 0.5) / 2^24 (exact
+// in float), score = x / t - log(max(-log u, 1e-10)) evaluated in double and rounded to float.
+__device__ __forceinline__ float perturbed(float x, float inv_t, uint32_t r) {
+    const float u = (static_cast<float>(r >> 8) + 0.5f) * (1.0f / 16777216.0f);
+    const double g = -log(fmax(-log(static_cast<double>(u)), 1e-10));
+    return static_cast<float>(static_cast<double>(x) * inv_t + g);
 }
 
-template <int LDT>
-__device__ __forceinline__ float load_logit(const void* row, int64_t j) {
-    if constexpr (LDT == CVH_DTYPE_F32) return static_cast<const float*>(row)[j];
-    else return bf16_bits_to_f32(static_cast<const uint16_t*>(row)[j]);
+template <int CTRL> __device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(v)), CTRL, 0xF, 0xF, true);
+    const uint32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(v >> 32)), CTRL, 0xF, 0xF, true);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// Max over the 64 lanes (every lane active): quad DPP, then mirrors (exact once quads / halves are
+// uniform), then the gfx950 permlane16/32 swaps across rows.
+__device__ __forceinline__ uint64_t wave_kmax(uint64_t v) {
+    v = kmax(v, dpp64<0xB1>(v));
+    v = kmax(v, dpp64<0x4E>(v));
+    v = kmax(v, dpp64<0x141>(v));
+    v = kmax(v, dpp64<0x140>(v));
+    uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+    auto l16 = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    auto h16 = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = kmax((static_cast<uint64_t>(h16[0]) << 32) | l16[0], (static_cast<uint64_t>(h16[1]) << 32) | l16[1]);
+    lo = static_cast<uint32_t>(v);
+    hi = static_cast<uint32_t>(v >> 32);
+    auto l32 = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    auto h32 = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return kmax((static_cast<uint64_t>(h32[0]) << 32) | l32[0], (static_cast<uint64_t>(h32[1]) << 32) | l32[1]);
 }
 
-// One workgroup per sampled row. Each thread scans groups of 8 logits (Philox counter = index/4,
-// so one group uses two Philox blocks), keeps its best (value, index), then the wave and the
-// workgroup reduce with the same tie rule.
+// The 8 logits at [j, j+8) of a row as float; positions past V read as -inf (never selected:
+// the caller does not fold them).
 template <int LDT>
-__global__ __launch_bounds__(kSampleThreads) void sample_kernel(int64_t* __restrict__ out, const void* __restrict__ logits,
-                                                                const int64_t* __restrict__ rows,
-                                                                const float* __restrict__ temps, int V,
-                                                                uint64_t seed, uint64_t offset) {
-    const int r = blockIdx.x;
-    const int64_t src = rows ? rows[r] : r;
-    const size_t esz = LDT == CVH_DTYPE_F32 ? 4 : 2;
-    const char* row = static_cast<const char*>(logits) + static_cast<size_t>(src) * V * esz;
-    const float temp = temps ? temps[r] : 0.f;
-    const bool greedy = !(temp > 0.f);
-    const float inv_t = 1.0f / fmaxf(temp, 1e-5f);
-    const bool vec = (V & 7) == 0;
-
-    Best best{-INFINITY, 0x7fffffff};
-    for (int base = threadIdx.x * 8; base < V; base += kSampleThreads * 8) {
-        float x[8];
-        if (vec && LDT != CVH_DTYPE_F32) {
-            const u32x4 w = ld_nt(row + static_cast<size_t>(base) * 2);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+__device__ __forceinline__ void logits8(const char* row, int j, int V, float* x) {
+    if (j + 8 <= V && (V & 7) == 0) {
+        if constexpr (LDT == CVH_DTYPE_F32) {
+            const u32x4 a = ld_nt(row + static_cast<size_t>(j) * 4);
+            const u32x4 b = ld_nt(row + static_cast<size_t>(j) * 4 + 16);
+            x[0] = __uint_as_float(a.x); x[1] = __uint_as_float(a.y); x[2] = __uint_as_float(a.z); x[3] = __uint_as_float(a.w);
+            x[4] = __uint_as_float(b.x); x[5] = __uint_as_float(b.y); x[6] = __uint_as_float(b.z); x[7] = __uint_as_float(b.w);
+        } else {
+            const u32x4 a = ld_nt(row + static_cast<size_t>(j) * 2);
+            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x[2 * j] = __uint_as_float(ws[j] << 16);
-                x[2 * j + 1] = __uint_as_float(ws[j] & 0xffff0000u);
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+                x[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
             }
-        } else if (vec) {
-            const f32x4 a = __builtin_bit_cast(f32x4, ld_nt(row + static_cast<size_t>(base) * 4));
-            const f32x4 b = __builtin_bit_cast(f32x4, ld_nt(row + static_cast<size_t>(base) * 4 + 16));
-            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-            x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = base + j < V ? load_logit<LDT>(row, base + j) : -INFINITY;
         }
-        if (greedy) {
+    } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (base + j < V && better(x[j], base + j, best)) best = {x[j], base + j};
-        } else {
+        for (int e = 0; e < 8; ++e) {
+            if (j + e >= V) { x[e] = -INFINITY; continue; }
+            if constexpr (LDT == CVH_DTYPE_F32) x[e] = reinterpret_cast<const float*>(row)[j + e];
+            else x[e] = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(row)[j + e]);
+        }
+    }
+}
+
+template <int LDT, bool GUMBEL>
+__device__ __forceinline__ uint64_t scan_slice(const char* row, int lo, int hi, int V, int lane, int r, float inv_t,
+                                               uint64_t seed, uint64_t offset) {
+    uint64_t best = rank_key(-INFINITY, 0x7fffffffu);
+    for (int j = lo + 8 * lane; j < hi; j += 8 * 64) {
+        float x[8];
+        logits8<LDT>(row, j, V, x);
+        uint32_t rnd[8];
+        if constexpr (GUMBEL) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int b4 = base + 4 * h;
-                uint32_t c[4] = {static_cast<uint32_t>(b4 >> 2), static_cast<uint32_t>(r), static_cast<uint32_t>(offset),
-                                 static_cast<uint32_t>(offset >> 32)};
+                // Philox counter (index / 4, row, offset): one block gives the words of 4 indices
+                uint32_t c[4] = {static_cast<uint32_t>((j >> 2) + h), static_cast<uint32_t>(r),
+                                 static_cast<uint32_t>(offset), static_cast<uint32_t>(offset >> 32)};
                 philox4x32_10(c, static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32));
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (b4 + j >= V) break;
-                    const float s = gumbel_score(x[4 * h + j], inv_t, c[j]);
-                    if (better(s, b4 + j, best)) best = {s, b4 + j};
-                }
+                for (int e = 0; e < 4; ++e) rnd[4 * h + e] = c[e];
             }
         }
-    }
 #pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-        const float ov = __shfl_xor(best.v, d, 64);
-        const int oi = __shfl_xor(best.i, d, 64);
-        if (better(ov, oi, best)) best = {ov, oi};
-    }
-    __shared__ float sv[kSampleThreads / 64];
-    __shared__ int si[kSampleThreads / 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        sv[wave] = best.v;
-        si[wave] = best.i;
-    }
-    __syncthreads();
-    if (wave == 0) {
-        best = lane < kSampleThreads / 64 ? Best{sv[lane], si[lane]} : Best{-INFINITY, 0x7fffffff};
-#pragma unroll
-        for (int d = 8; d > 0; d >>= 1) {
-            const float ov = __shfl_xor(best.v, d, 64);
-            const int oi = __shfl_xor(best.i, d, 64);
-            if (better(ov, oi, best)) best = {ov, oi};
+        for (int e = 0; e < 8; ++e) {
+            if (j + e >= hi) break;
+            const float s = GUMBEL ? perturbed(x[e], inv_t, rnd[e]) : x[e];
+            best = kmax(best, rank_key(s, static_cast<uint32_t>(j + e)));
         }
-        if (lane == 0) out[r] = best.i;
     }
+    return best;
+}
+
+template <int LDT>
+__global__ __launch_bounds__(64 * kSampleWaves) void sample_kernel(int64_t* __restrict__ out,
+                                                                   const void* __restrict__ logits,
+                                                                   const int64_t* __restrict__ rows,
+                                                                   const float* __restrict__ temps, int V,
+                                                                   uint64_t seed, uint64_t offset) {
+    __shared__ unsigned long long winner;
+    const int r = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (threadIdx.x == 0) winner = 0ull;
+    const int64_t src = rows ? rows[r] : r;
+    const char* row = static_cast<const char*>(logits) + static_cast<size_t>(src) * V * (LDT == CVH_DTYPE_F32 ? 4 : 2);
+    const float t = temps ? temps[r] : 0.f;
+    // contiguous slice of this wave, a multiple of 8 so a Philox block never straddles slices
+    const int slice = ((V + kSampleWaves * 8 - 1) / (kSampleWaves * 8)) * 8;
+    const int lo = wave * slice, hi = min(V, lo + slice);
+    uint64_t k = t > 0.f ? scan_slice<LDT, true>(row, lo, hi, V, lane, r, 1.0f / fmaxf(t, 1e-5f), seed, offset)
+                         : scan_slice<LDT, false>(row, lo, hi, V, lane, r, 0.f, seed, offset);
+    k = wave_kmax(k);
+    __syncthreads();
+    if (lane == 0) atomicMax(&winner, static_cast<unsigned long long>(k));
+    __syncthreads();
+    if (threadIdx.x == 0) out[r] = key_index(winner);
 }
 
 // ---- token feedback and embedding -------------------------------------------------------------
@@ -271,9 +306,9 @@ extern "C" int cvh_sample_tokens(int64_t* out, const void* logits, int logits_dt
     auto s = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(num_rows));
     if (logits_dtype == CVH_DTYPE_F32)
-        sample_kernel<CVH_DTYPE_F32><<<grid, kSampleThreads, 0, s>>>(out, logits, rows, temps, vocab, seed, offset);
+        sample_kernel<CVH_DTYPE_F32><<<grid, 64 * kSampleWaves, 0, s>>>(out, logits, rows, temps, vocab, seed, offset);
     else if (logits_dtype == CVH_DTYPE_BF16)
-        sample_kernel<CVH_DTYPE_BF16><<<grid, kSampleThreads, 0, s>>>(out, logits, rows, temps, vocab, seed, offset);
+        sample_kernel<CVH_DTYPE_BF16><<<grid, 64 * kSampleWaves, 0, s>>>(out, logits, rows, temps, vocab, seed, offset);
     else
         return CVH_ERR_UNSUPPORTED;
     return launched();

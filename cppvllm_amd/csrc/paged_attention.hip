@@ -15,7 +15,7 @@
 //     whole 1 KB slot rows (all heads of a token) are read together.
 //   * a row piece that is cut by a workgroup boundary is written as an (acc, max, sum) partial to
 //     one of two per-workgroup slots (0: the piece containing the workgroup's first tile, 1: the
-//     one containing its last); whole rows are finished in place. paged_merge_kernel combines
+//     one containing its last); whole rows are finished in place. paged_merge2_kernel combines
 //     the pieces of cut rows.
 //
 // Per wave (one kv head, REP query heads), designed for wave64:
@@ -219,8 +219,10 @@ struct Params {
     float q_scale;           // softmax scale * log2(e)
 };
 
-// Causal length of token t, clamped to what its block-table row can address.
-__device__ __forceinline__ int token_len(const Params& p, int t) {
+// Causal length of token t, clamped to what its block-table row can address. A padding token
+// (token_seq < 0) has length 0 whatever its kv_len says, so its output row is zero.
+__device__ __forceinline__ int token_len(const Params& p, int t, int64_t seq) {
+    if (seq < 0) return 0;
     int64_t kv = p.token_kv_len[t];
     const int64_t cap = p.table_width << p.log2_bs;
     if (kv > cap) kv = cap;
@@ -249,7 +251,7 @@ __device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int 
     const int tid = threadIdx.x;
     for (int t = tid; t < p.num_tokens; t += nthreads) {
         const int64_t sq = p.token_seq[t];
-        tok[t] = make_int2(token_len(p, t), static_cast<int>(sq > 0 ? sq : 0));
+        tok[t] = make_int2(token_len(p, t, sq), static_cast<int>(sq > 0 ? sq : 0));
     }
     __syncthreads();
     const int per = (rows + nthreads - 1) / nthreads;
@@ -841,63 +843,12 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 
 // Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One workgroup
 // per row (token, kv-head group): it recomputes, from the prefix the decode kernel stored, which
-// workgroups covered the row (wave-uniform scalar arithmetic) and exits if one did. Otherwise
-// thread i handles query head i / (HD/4) of the row and 4 consecutive dims; the pieces are
-// combined in one online pass (running max), so their loads are independent of each other.
-template <int HD, int SM>
-__global__ __launch_bounds__(512) void paged_merge_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
-                                                          const float* __restrict__ part_ml,
-                                                          const int* __restrict__ prefix,
-                                                          const float* __restrict__ v_scale, int num_tokens, int n_kv,
-                                                          int rep, int wpg, int G) {
-    constexpr int TPH = HD / 4;                       // threads per query head
-    const int row = blockIdx.x;
-    const int hg_count = n_kv / wpg;
-    const int heads_per_row = wpg * rep;             // query heads of one row group
-    const int rows = num_tokens * hg_count;
-    const int64_t U = prefix[rows];
-    const int64_t pr0 = prefix[row], pr1 = prefix[row + 1];
-    if (pr1 == pr0) return;
-    // workgroup holding tile u: the largest w with w*U/G <= u
-    auto owner = [&](int64_t u) { return static_cast<int>(((u + 1) * G - 1) / U); };
-    const int w0 = owner(pr0), w1 = owner(pr1 - 1);
-    if (w0 == w1) return;
-    const int t = row / hg_count, hgi = row % hg_count;
-    const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
-    for (int hh = threadIdx.x / TPH; hh < heads_per_row; hh += blockDim.x / TPH) {
-        const int d0 = (threadIdx.x % TPH) * 4;
-        float M = kMinusHuge, L = 0.f;
-        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-        for (int w = w0; w <= w1; ++w) {
-            // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
-            if (w * U / G == (w + 1) * U / G) continue;
-            const int slot = (pr0 <= w * U / G) ? 0 : 1;
-            const int64_t idx = (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh;
-            const float2 ml = reinterpret_cast<const float2*>(part_ml)[idx];
-            const float4 a = *reinterpret_cast<const float4*>(part_acc + idx * HD + d0);
-            const float Mn = fmaxf(M, ml.x);
-            const float co = exp2f(M - Mn), cn = exp2f(ml.x - Mn);
-            L = L * co + ml.y * cn;
-            A.x = A.x * co + a.x * cn;
-            A.y = A.y * co + a.y * cn;
-            A.z = A.z * co + a.z * cn;
-            A.w = A.w * co + a.w * cn;
-            M = Mn;
-        }
-        const float f = vfin / L;
-        const int h = hgi * heads_per_row + hh;      // query head index within the token
-        uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
-        const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
-        const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
-        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
-    }
-}
-
-// Two halves of 512 threads per row (every thread one head slice, so the halves' loops agree in
-// length): half p folds pieces w0 + p, w0 + p + 2, ... online, then half 1 hands its (M, L, A)
-// to half 0 through LDS, which combines the two; a row's chain of dependent piece loads is half
-// as long (small batches cut a row into up to 8 pieces).
+// workgroups covered the row (wave-uniform scalar arithmetic) and exits if one did. The workgroup
+// is two halves with one thread per (query head, 4 dims) of the row each (wpg * rep * HD / 4 <=
+// 512 for every supported shape: wpg <= 8, rep <= 2 after the virtual-head split, HD <= 128);
+// half p folds pieces w0 + p, w0 + p + 2, ... online, then half 1 hands its (M, L, A) to half 0
+// through LDS, which combines the two, so a row's chain of dependent piece loads is half as long
+// (small batches cut a row into up to 8 pieces).
 template <int HD, int SM>
 __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
                                                           const float* __restrict__ part_ml,
@@ -1224,42 +1175,22 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     }
     if ((phase & kPhaseMerge) && G > 1) {
         const dim3 mgrid(static_cast<unsigned>(rows));
-        // one thread per 4 output dims of the row's wpg*rep heads, up to 512 (more heads loop)
-        const int mthreads = std::min(512, wpg * rep_v * head_dim / 4);
         const int nt = static_cast<int>(num_tokens);
-        // every thread one head slice: two halves split the row's pieces
-        if (wpg * rep_v * head_dim / 4 <= 512) {
-            const int m2 = 2 * (wpg * rep_v * head_dim / 4);
-            if (head_dim == 128) {
-                if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                    paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
-                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
-                else
-                    paged_merge2_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
-                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
-            } else {
-                if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                    paged_merge2_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
-                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
-                else
-                    paged_merge2_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
-                            p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
-            }
-            return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
-        }
+        const int m2 = 2 * (wpg * rep_v * head_dim / 4);   // two halves, one thread per head slice
+        static_assert(8 * 2 * 128 / 4 <= 512, "wpg <= 8, rep_v <= 2, HD <= 128: one slice per thread");
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
+                paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
             else
-                paged_merge_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, mthreads, 0, s>>>(
+                paged_merge2_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
         } else {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-                paged_merge_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, mthreads, 0, s>>>(
+                paged_merge2_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
             else
-                paged_merge_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, mthreads, 0, s>>>(
+                paged_merge2_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
                         p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
         }
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
@@ -1270,10 +1201,14 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
 }  // namespace
 }  // namespace cvh
 
-extern "C" int cvh_paged_attention_partitions(int64_t num_tokens, int n_kv_heads, int64_t table_width,
+extern "C" int cvh_paged_attention_partitions(int64_t num_tokens, int n_heads, int n_kv_heads, int64_t table_width,
                                               int block_size) {
-    if (num_tokens <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0) return 1;
-    return cvh::auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
+    if (num_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0 ||
+        n_heads % n_kv_heads != 0)
+        return 1;
+    const int rep = n_heads / n_kv_heads;
+    const int n_kv = n_kv_heads * (rep > 2 ? rep / 2 : 1);   // the kernel's (virtual) kv heads, as in the launch
+    return cvh::auto_partitions(num_tokens, n_kv, table_width, block_size);
 }
 
 extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
@@ -1351,3 +1286,4 @@ extern "C" int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* 
                                       token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size, scale_mode,
                                       scale, 0, workspace, workspace_bytes, stream);
 }
+

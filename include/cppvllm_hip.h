@@ -54,7 +54,9 @@ enum { CVH_DTYPE_BF16 = 0, CVH_DTYPE_F16 = 1, CVH_DTYPE_F32 = 2 };
  *   out          bf16 [num_tokens][n_heads][head_dim]
  *   q            bf16 [num_tokens][n_heads][head_dim]
  *   block_tables int64 [num_seqs][table_width]; entries past a sequence's last block are ignored
- *   token_seq    int64 [num_tokens]  row of block_tables for each query token
+ *   token_seq    int64 [num_tokens]  row of block_tables for each query token; a negative value
+ *                                    marks a padding token, whose output row is all zero whatever
+ *                                    its kv_len (the same rule in every attention entry point)
  *   token_kv_len int64 [num_tokens]  causal context length of each query token (positions+1);
  *                                    a token with kv_len <= 0 gets an all-zero output row
  *   scale        softmax scale (1/sqrt(head_dim) in the reference)
@@ -182,8 +184,10 @@ int cvh_paged_attention_fp8_planned_split_phase(void* out, const void* q, const 
 size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
                                            int64_t table_width, int block_size, int partitions);
 
-/* The partition count the automatic policy picks for these shapes. */
-int cvh_paged_attention_partitions(int64_t num_tokens, int n_kv_heads, int64_t table_width, int block_size);
+/* The partition count the automatic policy picks for these shapes (the same count the launches
+ * and cvh_paged_attention_workspace_bytes use for partitions = 0). */
+int cvh_paged_attention_partitions(int64_t num_tokens, int n_heads, int n_kv_heads, int64_t table_width,
+                                   int block_size);
 
 /* ---------------------------------------------------------------------------------------------
  * RMSNorm family. Replaces fused::rms_norm / fused::add_rms_norm (kernels/fused_ops.h:7-9,

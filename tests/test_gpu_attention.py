@@ -155,6 +155,28 @@ def test_empty_context_rows_are_zero(orc):
     assert_close_bf16(got[:1], run_oracle(orc, b, rows=[0]))
 
 
+@pytest.mark.parametrize("mode", ["plain", "planned", "partitions_64"])
+def test_padding_rows_are_zero(orc, mode):
+    """token_seq < 0 marks a padding token: its output row is zero whatever its kv_len says (the
+    same rule as the prefill kernel and the oracle), and the other rows are unaffected."""
+    say(f"padding rows (token_seq -1, kv_len > 0): {mode}")
+    b = synth(6, [300, 50, 1000, 700, 17], 16)
+    b["token_seq"][1] = -1
+    b["token_seq"][3] = -1
+    b["token_kv_len"][3] = 4000          # beyond any table row: must not matter either
+    db = dev(b)
+    if mode == "planned":
+        got = run_planned(db)
+    else:
+        got = run_gpu(db, 64 if mode == "partitions_64" else 0)
+    assert not got[1].any() and not got[3].any()
+    assert_close_bf16(got, run_oracle(orc, b))
+    keep = [0, 2, 4]
+    b2 = {k: v for k, v in b.items()}
+    b2["q"], b2["token_seq"], b2["token_kv_len"] = b["q"][keep], b["token_seq"][keep], b["token_kv_len"][keep]
+    assert_close_bf16(got[keep], run_gpu(dev(b2)), max_abs=8e-3, mean_abs=5e-4)
+
+
 def test_block_permutation_invariance_bitwise():
     say("physical block permutation invariance")
     b = synth(31, [500, 900, 17], 16)
@@ -184,10 +206,11 @@ def test_config4_long_context(orc, shared):
     b = workloads.config4(device=DEV, shared_prefix=shared)
     got = run_gpu(b)
     assert np.isfinite((got.astype(np.uint32) << 16).view(np.float32)).all()
-    rows = [0, 1, 2, 7, 30, 63]
     bc = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in b.items()}
-    want = run_oracle(orc, bc, rows=rows)
-    assert_close_bf16(got[rows], want)
+    # all 64 rows; outputs dominated by 20x outliers reach |x| > 4, where one bf16 ulp exceeds
+    # 2e-2 and a value near a rounding midpoint legitimately rounds either way (row 43 of the
+    # unshared case: exact -17.436, GPU -17.375, oracle -17.5)
+    assert_close_bf16(got, run_oracle(orc, bc), ulp_floor=True)
     if shared:
         t = bc["block_tables"]
         assert (t[0, :8] == t[2, :8]).all() and (t[0, :8] == t[62, :8]).all()
@@ -467,9 +490,8 @@ def test_shared_prefix_plan_is_bitwise_identical(orc):
         torch.cuda.synchronize()
         outs.append(bits(out))
     assert np.array_equal(outs[0], outs[1])
-    rows = [0, 1, 2, 3, 62, 63]
-    assert_close_bf16(outs[1][rows], run_oracle(orc, {k: (v.cpu() if isinstance(v, torch.Tensor) else v)
-                                                     for k, v in b.items()}, rows=rows))
+    assert_close_bf16(outs[1], run_oracle(orc, {k: (v.cpu() if isinstance(v, torch.Tensor) else v)
+                                               for k, v in b.items()}), ulp_floor=True)
 
 
 @pytest.mark.parametrize("tp", [2, 4, 8])

@@ -33,8 +33,19 @@ def _fp8_fake(x):
     return q * sc
 
 
-def ref_forward(m, tokens, positions):
-    """Plain torch fp32 Qwen3 forward of ONE sequence (all its tokens), returns the final-normed x."""
+def _linear_bf16(x, w):
+    return F.linear(x, w)
+
+
+def linear_f64(x, w):
+    """x . w^T with float64 accumulation, rounded to bf16: the same rounding points as a bf16
+    GEMM with another (exact) summation order."""
+    return (x.double() @ w.double().T).to(torch.bfloat16)
+
+
+def ref_forward(m, tokens, positions, linear=_linear_bf16):
+    """Plain torch fp32 Qwen3 forward of ONE sequence (all its tokens), returns the final-normed x.
+    linear: the bf16 GEMM (torch's by default)."""
     c = m.cfg
     H, KV, HD, eps = c.n_heads, c.n_kv_heads, c.head_dim, c.norm_eps
     T = tokens.numel()
@@ -50,7 +61,7 @@ def ref_forward(m, tokens, positions):
     x = _rms(h, m.attn_norm[0], eps)
     mask = torch.ones(T, T, dtype=torch.bool, device=h.device).tril()
     for li in range(c.n_layers):
-        qkv = F.linear(bf(x), m.wqkv[li]).float()
+        qkv = linear(bf(x), m.wqkv[li]).float()
         q = qkv[:, :H * HD].view(T, H, HD)
         k = qkv[:, H * HD:(H + KV) * HD].view(T, KV, HD)
         v = qkv[:, (H + KV) * HD:].view(T, KV, HD)
@@ -62,13 +73,13 @@ def ref_forward(m, tokens, positions):
         s = torch.einsum("thd,shd->hts", q, k) / math.sqrt(HD)
         s = s.masked_fill(~mask, float("-inf"))
         att = torch.einsum("hts,shd->thd", s.softmax(-1), v)
-        o = F.linear(bf(att).reshape(T, H * HD), m.wo[li]).float()
+        o = linear(bf(att).reshape(T, H * HD), m.wo[li]).float()
         h = bf(h + o).float()
         x = _rms(h, m.ffn_norm[li], eps)
-        gu = F.linear(bf(x), m.w_gate_up[li]).float()
+        gu = linear(bf(x), m.w_gate_up[li]).float()
         g, u = gu[:, :c.intermediate_size], gu[:, c.intermediate_size:]
         act = bf(F.silu(g)).float() * u
-        mm = F.linear(bf(act), m.w_down[li]).float()
+        mm = linear(bf(act), m.w_down[li]).float()
         h = bf(h + mm).float()
         nxt = m.attn_norm[li + 1] if li + 1 < c.n_layers else m.final_norm
         x = _rms(h, nxt, eps)

@@ -56,6 +56,10 @@ def test_greedy_sampler_full_vocab(orc, ldtype):
     lg[5, 0] = 60.0
     lg[6, :] = float("-inf")
     lg[7, 5] = float("nan")
+    lg[8, :] = float("nan")                       # nothing wins: the (-inf, 0x7FFFFFFF) start stays
+    lg[9, :] = float("nan")
+    lg[9, 70000] = float("-inf")                  # -inf beats NaN
+    lg[10, :] = 1.0                               # all equal: index 0
     out = torch.empty(R, dtype=torch.int64, device=DEV)
     ops.fused.sample_tokens(out, lg.to(DEV), None, None, 0, 0)
     torch.cuda.synchronize()
@@ -64,12 +68,13 @@ def test_greedy_sampler_full_vocab(orc, ldtype):
     bad = np.nonzero(got != want)[0]
     assert bad.size == 0, f"rows {bad[:8]}: got {got[bad[:8]]} want {want[bad[:8]]}"
     assert want[3] == 17 and want[4] == V - 1 and want[5] == 0 and want[6] == 0
+    assert want[8] == 0x7FFFFFFF and want[9] == 70000 and want[10] == 0
 
 
 def test_sampler_rows_and_temperatures(orc):
-    say("gumbel sampler rows/temps R=8 V=151936 and V=1003")
+    say("gumbel sampler rows/temps R=8 V=151936, 1003, 8, 7, 1")
     g = torch.Generator().manual_seed(12)
-    for V in (151936, 1003):
+    for V in (151936, 1003, 8, 7, 1):
         lg = torch.randn((10, V), generator=g)
         rows = torch.tensor([9, 0, 3, 3, 5, 1, 2, 8], dtype=torch.int64)
         temps = torch.tensor([0.6, 1.0, 0.0, 0.6, 2.0, -1.0, 1e-6, 0.3], dtype=torch.float32)

@@ -118,7 +118,7 @@ def test_partition_policy_and_workspace_sizes():
     lib = _lib.lib()
     # headline decode (256 tokens, 8 kv heads = one 8-wave row group, 8 x 256-token blocks):
     # 256 partitions (2048 resident waves / 8)
-    assert lib.cvh_paged_attention_partitions(256, 8, 8, 256) == 256
+    assert lib.cvh_paged_attention_partitions(256, 16, 8, 8, 256) == 256
     rows, slots = 256, 256 * 2 * 16     # [G][2][WPG*REP] partial slots
     r256 = lambda v: (v + 255) // 256 * 256
     # plan: int2 token metadata [T] + int32 shared-prefix keys [T] + 184-byte workgroup records [G]
@@ -133,13 +133,19 @@ def test_partition_policy_and_workspace_sizes():
             r256(256 * 2 * H // (vrows // 256) * 2 * 4) + r256(256 * 8) + r256(256 * 4) + r256(256 * 184)
         assert lib.cvh_paged_attention_workspace_bytes(256, H, 8, 128, 8, 256, 0) == want_v, H
     # small batches: never less than two tiles per partition
-    assert lib.cvh_paged_attention_partitions(1, 1, 1, 16) == 1
+    assert lib.cvh_paged_attention_partitions(1, 1, 1, 1, 16) == 1
     # few rows: at most 8 partitions per row (8 rows -> 64, though 2 tiles each would allow 128)
-    assert lib.cvh_paged_attention_partitions(8, 8, 4, 256) == 64
-    assert lib.cvh_paged_attention_partitions(16, 8, 8, 256) == 128
+    assert lib.cvh_paged_attention_partitions(8, 16, 8, 4, 256) == 64
+    assert lib.cvh_paged_attention_partitions(16, 16, 8, 8, 256) == 128
     # one kv head: one-wave workgroups, capped at 1024 (not one per resident wave slot, 2048)
-    assert lib.cvh_paged_attention_partitions(256, 1, 8, 256) == 1024
-    assert lib.cvh_paged_attention_partitions(256, 2, 8, 256) == 1024
+    assert lib.cvh_paged_attention_partitions(256, 2, 1, 8, 256) == 1024
+    assert lib.cvh_paged_attention_partitions(256, 4, 2, 8, 256) == 1024
+    # GQA 4: the policy sees the launch's virtual kv heads (16 = 2 row groups per token), so 16
+    # tokens give 32 rows and up to 8 partitions each: 256, as the launch and workspace size use
+    assert lib.cvh_paged_attention_partitions(16, 32, 8, 8, 256) == 256
+    r16 = r256(33 * 4) + r256(256 * 2 * 16 * 128 * 4) + r256(256 * 2 * 16 * 2 * 4) + r256(16 * 8) + \
+        r256(16 * 4) + r256(256 * 184)
+    assert lib.cvh_paged_attention_workspace_bytes(16, 32, 8, 128, 8, 256, 0) == r16
     assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 8, 16, -1) == 0
 
 
