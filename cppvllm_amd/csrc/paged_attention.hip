@@ -39,6 +39,7 @@
 
 #include <algorithm>
 #include <cstddef>
+#include <mutex>
 #include <type_traits>
 
 #include "cvh_device.h"
@@ -1287,3 +1288,67 @@ extern "C" int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* 
                                       scale, 0, workspace, workspace_bytes, stream);
 }
 
+// ---- no-allocation entry point ------------------------------------------------------------------
+// The split workspace of cvh_paged_attention_fp8 lives here instead of in a caller buffer: a
+// file-scope device array, one copy per GPU, alive until the process ends. Host code must not use
+// the array's name as an address (it is a host-side stand-in); the device address is looked up
+// once per device with hipGetSymbolAddress and cached. Nothing in the workspace needs to start at
+// zero (every launch writes what it later reads), so calls clear nothing; calls that overlap on
+// one GPU (two streams, or two host threads) share the array and race.
+namespace cvh {
+namespace {
+// 8 MiB. With automatic partitions every supported launch fits: partials are at most
+// G * 2 * (heads per row group) <= (2048 / wpg) * 2 * (2 * wpg) = 8192 slots of HD floats (4 MiB at
+// HD 128), plus the prefix, token and plan records of at most 8192 rows (< 0.5 MiB). Explicit
+// partition counts beyond that are rejected.
+constexpr size_t kScratchBytes = size_t{8} << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+}  // namespace cvh
+
+static __device__ __align__(256) unsigned char scratch[cvh::kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[cvh::kMaxDevices] = {};
+
+// Device address of this GPU's scratch array (looked up on the first call on each device, with
+// that device current), or nullptr if the lookup failed.
+void* device_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= cvh::kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" size_t cvh_paged_attention_noalloc_max_workspace(void) { return cvh::kScratchBytes; }
+
+extern "C" int cvh_paged_attention_fp8_noalloc(void* out, const void* q, const uint8_t* k_cache,
+                                               const uint8_t* v_cache, const float* k_scale, const float* v_scale,
+                                               const int64_t* block_tables, int64_t table_width,
+                                               const int64_t* token_seq, const int64_t* token_kv_len,
+                                               int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                               int block_size, int scale_mode, double scale, int partitions,
+                                               cvh_stream_t stream) {
+    if (num_tokens == 0) return CVH_OK;
+    if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0 || partitions < 0)
+        return CVH_ERR_INVALID_ARG;
+    const size_t need = cvh_paged_attention_workspace_bytes(num_tokens, n_heads, n_kv_heads, head_dim, table_width,
+                                                            block_size, partitions);
+    if (need == 0) return CVH_ERR_INVALID_ARG;
+    if (need > cvh::kScratchBytes) return CVH_ERR_WORKSPACE;   // beyond the fixed array: use cvh_paged_attention_fp8_ex
+    void* ws = device_scratch();
+    if (ws == nullptr) return CVH_ERR_LAUNCH;
+    return cvh::paged_attention(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq,
+                                token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size, scale_mode, scale,
+                                partitions, ws, cvh::kScratchBytes, stream, cvh::kPhaseBoth);
+}

@@ -179,6 +179,23 @@ int cvh_paged_attention_fp8_planned_split_phase(void* out, const void* q, const 
                                                 int block_size, int scale_mode, double scale, int partitions,
                                                 void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 
+/* cvh_paged_attention_fp8_ex without a workspace argument: the split workspace is a fixed 8 MiB
+ * device array inside the library (one per GPU, held until the process ends), so the call allocates
+ * nothing and needs no caller buffer. No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Every launch with automatic partitions (partitions = 0) fits; a partition count whose
+ * workspace (cvh_paged_attention_workspace_bytes) exceeds cvh_paged_attention_noalloc_max_workspace()
+ * returns CVH_ERR_WORKSPACE before anything runs. Results equal cvh_paged_attention_fp8_ex bit for
+ * bit. All calls on one GPU share the array and leave their data in it (nothing in it needs to start
+ * at zero): calls that overlap on one GPU (two streams or two host threads) race. */
+int cvh_paged_attention_fp8_noalloc(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                    const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                    int64_t table_width, const int64_t* token_seq, const int64_t* token_kv_len,
+                                    int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
+                                    int scale_mode, double scale, int partitions, cvh_stream_t stream);
+/* Bytes of that fixed array (the largest workspace cvh_paged_attention_fp8_noalloc accepts). */
+size_t cvh_paged_attention_noalloc_max_workspace(void);
+
 /* Workspace bytes needed by the calls above (replaces the per-call at::empty of
  * kernels/paged_attention.cu:415-421, which cannot run under graph capture). */
 size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
