@@ -394,6 +394,8 @@ def main():
     ap.add_argument("--seqs", type=int, default=256,
                     help="config 3 with this many sequences (a smaller decode batch; the headline is 256)")
     ap.add_argument("--shared-prefix", action="store_true", help="config 4b: even sequences share 8 blocks")
+    ap.add_argument("--gqa", type=int, default=0, choices=(0, 1, 2, 4, 8),
+                    help="query heads per kv head over the same K/V (0: the workload's own, 2)")
     ap.add_argument("--tp", type=int, default=1, choices=(1, 2, 4, 8),
                     help="configs 3/4 at one GPU's tensor-parallel share: kv heads 8/tp, query heads 16/tp")
     ap.add_argument("--no-shared-reuse", action="store_true",
@@ -448,6 +450,11 @@ def main():
         b = workloads.config4(device=dev, shared_prefix=args.shared_prefix)
     if args.tp > 1:
         b = workloads.tp_share(b, args.tp)
+    if args.gqa:
+        # the same K/V read by gqa query heads per kv head (GQA ratio args.gqa)
+        g = torch.Generator(device=dev).manual_seed(77)
+        b["n_heads"] = b["n_kv_heads"] * args.gqa
+        b["q"] = torch.randn((b["q"].shape[0], b["n_heads"], b["head_dim"]), generator=g, device=dev).to(torch.bfloat16)
     lens = b["token_kv_len"].cpu().tolist()
     T, H, KV, HD, BS = len(lens), b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
     W = b["block_tables"].shape[1]
@@ -568,7 +575,7 @@ def main():
             else None,
             "seqs": T, "ctx_sum": int(sum(lens)), "ctx_min": int(min(lens)), "ctx_max": int(max(lens)),
             "n_heads": H, "n_kv_heads": KV, "head_dim": HD, "block_size": BS, "layers": len(layer_ptrs),
-            "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, H, KV, W, BS)
+            "scale_mode": "per_token_head", "partitions": lib.cvh_paged_attention_partitions(T, H, KV, HD, W, BS)
             if args.partitions == 0 else args.partitions,
             "bytes_per_layer": bytes_layer, "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
             "launch": "eager" if args.eager else "hip_graph",

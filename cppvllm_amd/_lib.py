@@ -54,7 +54,7 @@ SIGNATURES = {
                                               f64, i32, vp]),
     "cvh_paged_attention_noalloc_max_workspace": (sz, []),
     "cvh_paged_attention_workspace_bytes": (sz, [i64, i32, i32, i32, i64, i32, i32]),
-    "cvh_paged_attention_partitions": (i32, [i64, i32, i32, i64, i32]),
+    "cvh_paged_attention_partitions": (i32, [i64, i32, i32, i32, i64, i32]),
     "cvh_rms_norm": (i32, [vp, vp, vp, i64, i32, f64, i32, vp]),
     "cvh_add_rms_norm": (i32, [vp, vp, vp, vp, i64, i32, f64, i32, vp]),
     "cvh_qk_norm_rope_kv_write_fp8": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i32, i32,

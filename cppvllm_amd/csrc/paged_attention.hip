@@ -53,6 +53,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;  // log2 units: stale max tolerated up to p = 2^8
 constexpr float kMinusHuge = -1e30f;
 constexpr int kMaxRows = 8192;             // rows (tokens x head groups) per launch: LDS prefix
+constexpr size_t kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
 constexpr int kMaxQRows = 8;
 constexpr int kPreQRows = 4;               // q rows a planned launch fetches ahead of its first tiles
@@ -93,8 +94,59 @@ template <> __device__ __forceinline__ uint2 buf_load<uint2, kTemporal>(__amdgpu
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kNonTemporal));
 }
+template <int POL> __device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL));
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// ---- GQA 4 / 8 on matrix cores (head_dim 128) ----------------------------------------------------
+// One wave per (query token, kv head) as in the VALU path, but the REP query heads of the kv head are
+// the 16 columns of v_mfma_f32_16x16x32_bf16 tiles (padded with zero columns):
+//   S^T[key][head] = K . Q^T : A = K (16 keys x 32 d, e4m3 -> bf16 exact), B = Q^T (bf16)
+//   O[head][d]    += P . V   : A = P (16 heads x 32 keys, bf16, V scale folded in), B = V (32 keys x 16 d)
+// Lane (i16 = lane % 16, g = lane / 16). In S^T a lane holds one head (column i16) for keys
+// {kb*16 + 4g + r}; those 8 keys are exactly the contraction slots 8g..8g+7 of the PV product's A
+// operand, so P never leaves its lane. V's B operand wants 8 keys of one d per lane: the lane loads
+// 8 bytes (d = 8*i16 .. +8) of each of its 8 keys, transposes the 4 key x 4 d byte blocks with
+// v_perm_b32, and feeds d = 8*i16 + j to the MFMA j (j = 0..7), whose output holds heads 4g..4g+3 of
+// that d in the lane. Softmax state is per S^T column (one head per lane, combined over the 4 lane
+// groups with permlane swaps); the rare rescale of O rows and the final normalisation fetch the 4
+// heads' factors with ds_bpermute. Loads per lane and 32-key tile: 4 x 16 B of K, 8 x 8 B of V and
+// 4 scales (lane r of each row of 16 loads key 4g + r's; the row reads them with DPP broadcasts).
+struct MfTile {
+    uint4 k[2][2];          // [kb][half]: key kb*16 + i16, bytes half*64 + g*16 .. +16 of the head's row
+    uint2 v[2][4];          // [kb][r]: key kb*16 + 4g + r, bytes 8*i16 .. +8
+    float ks[2], vs[2];     // [kb]: key kb*16 + 4g + (i16 & 3); lane r of each row of 16 is broadcast
+};
+// value of lane r of this lane's row of 16 (DPP row_newbcast)
+template <int R> __device__ __forceinline__ float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + R, 0xF, 0xF, false));
+}
+template <bool HI> __device__ __forceinline__ uint32_t fp8x2_bf16(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+// 8 e4m3 codes (bytes of lo, then hi) -> bf16x8, exact
+__device__ __forceinline__ bf16x8_t fp8x8_bf16(uint32_t lo, uint32_t hi) {
+    const uint4 u = make_uint4(fp8x2_bf16<false>(lo), fp8x2_bf16<true>(lo), fp8x2_bf16<false>(hi), fp8x2_bf16<true>(hi));
+    return __builtin_bit_cast(bf16x8_t, u);
+}
+// 4x4 byte transpose: w[r] holds bytes (r, 0..3); returns u[j] with bytes (0..3, j)
+__device__ __forceinline__ void transpose4x4(const uint32_t (&w)[4], uint32_t (&u)[4]) {
+    const uint32_t a = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);   // w0b0 w1b0 w0b1 w1b1
+    const uint32_t b = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);   // w0b2 w1b2 w0b3 w1b3
+    const uint32_t c = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+    const uint32_t d = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+    u[0] = __builtin_amdgcn_perm(c, a, 0x05040100u);
+    u[1] = __builtin_amdgcn_perm(c, a, 0x07060302u);
+    u[2] = __builtin_amdgcn_perm(d, b, 0x05040100u);
+    u[3] = __builtin_amdgcn_perm(d, b, 0x07060302u);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+    return f32_to_bf16_bits(lo) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+}
 
 template <int HD> struct KvVec;
 template <> struct KvVec<128> {
@@ -240,8 +292,13 @@ __host__ __device__ inline size_t lds_q_offset(int rows, int tokens) {
 }
 inline int q_stage_rows(int wpg, int rep, int hd) {
     const int per_row = wpg * rep * hd * 2;
-    return std::max(1, std::min(kMaxQRows, kQStageBytes / per_row));
+    // the MFMA path (rep >= 4) stages up to 4 rows of 8 heads x 8 waves (64 KiB)
+    const int budget = rep >= 4 ? 4 * kQStageBytes : kQStageBytes;
+    return std::max(1, std::min(kMaxQRows, budget / per_row));
 }
+// GQA 4 and 8 run on MFMA at head_dim 128; elsewhere (head_dim 64) as 2 / 4 virtual kv heads of 2
+// query heads (VALU path). Returns the number of virtual kv heads per physical one.
+inline int virtual_kv_split(int rep, int head_dim) { return (rep > 2 && head_dim != 128) ? rep / 2 : 1; }
 
 // Token metadata and the exclusive prefix of row tile counts into LDS (prefix[0..rows]); all
 // threads of the block. kv_len and the block-table row of every token are fetched together (one
@@ -359,10 +416,14 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const uint32_t srow_bytes = 4u << log2_bs;                      // scale row of one (block, head)
     const int bs_mask = (1 << log2_bs) - 1;
 
-    struct Tile {
+    constexpr bool MF = REP >= 4;                   // GQA 4 / 8: score and PV products on MFMA
+    static_assert(!MF || HD == 128, "the MFMA path is laid out for head_dim 128");
+    struct VTile {
         VT k[kSteps], v[kSteps];
         float ks[kSteps], vs[kSteps];
     };
+    using Tile = std::conditional_t<MF, MfTile, VTile>;
+    const int i16 = lane & 15, g4 = lane >> 4;      // MFMA lane coordinates
     // Physical blocks of a tile: `lo` for its first 16 keys, `hi` for the last 16 (equal unless
     // block_size == 16). Wave-uniform scalar loads, issued one tile ahead of the loads using them.
     struct Phys {
@@ -399,6 +460,33 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         const int p0 = tile * kTileKeys;
         const uint32_t lv = static_cast<uint32_t>(live);             // arithmetic, not a branch
         const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
+        if constexpr (MF) {
+            const uint32_t col = static_cast<uint32_t>(pc.g) * HD;   // the kv head's 128 bytes in a slot row
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int64_t ph = (ONE_BLOCK || kb == 0) ? ph2.lo : ph2.hi;
+                const auto rk = make_rsrc(p.k_cache + ph * blk_bytes, kv_rec);
+                const auto rv = make_rsrc(p.v_cache + ph * blk_bytes, kv_rec);
+                const uint32_t kin = static_cast<uint32_t>(min(p0 + kb * 16 + i16, pc.kv_len - 1) & bs_mask);
+                const uint32_t koff = kin * row_bytes + col + g4 * 16;
+                tl.k[kb][0] = buf_load<uint4, POL>(rk, koff);
+                tl.k[kb][1] = buf_load<uint4, POL>(rk, koff + 64);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t vin = static_cast<uint32_t>(min(p0 + kb * 16 + 4 * g4 + r, pc.kv_len - 1) & bs_mask);
+                    tl.v[kb][r] = buf_load<uint2, POL>(rv, vin * row_bytes + col + 8 * i16);
+                }
+                if constexpr (SM == CVH_SCALE_PER_TOKEN_HEAD) {
+                    const int64_t sbase = (ph * n_kv_phys + pc.g) << log2_bs;
+                    const uint32_t sin = static_cast<uint32_t>(min(p0 + kb * 16 + 4 * g4 + (i16 & 3), pc.kv_len - 1) & bs_mask);
+                    tl.ks[kb] = buf_load_f32(make_rsrc(p.k_scale + sbase, s_rec), sin * 4u);
+                    tl.vs[kb] = buf_load_f32(make_rsrc(p.v_scale + sbase, s_rec), sin * 4u);
+                } else {
+                    tl.ks[kb] = 1.f;
+                    tl.vs[kb] = 1.f;
+                }
+            }
+        } else {
         const uint32_t lane_col = (pc.g >> kv_shift) * HD + sub * E;   // byte column inside a slot row
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
@@ -416,6 +504,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 tl.ks[s] = 1.f;
                 tl.vs[s] = 1.f;
             }
+        }
         }
     };
 
@@ -596,33 +685,123 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(src + o);
         }
     };
-    uint32_t qf[REP][QW];
+    uint32_t qf[MF ? 1 : REP][QW];
+    bf16x8_t qm[MF ? 4 : 1];                        // MFMA B operands: step st covers d = (st>>1)*64 + g*16 + (st&1)*8 .. +8
     auto take_q = [&](const Piece& pc) {
         const uint16_t* src = q_lds + ((pc.row - rb) * wpg + wi) * (REP * HD);
+        if constexpr (MF) {
+            const bool head = i16 < REP;            // columns past REP are zero padding
 #pragma unroll
-        for (int r = 0; r < REP; ++r)
-#pragma unroll
-            for (int c = 0; c < E / 8; ++c) {
-                const uint4 u = *reinterpret_cast<const uint4*>(src + r * HD + sub * E + 8 * c);
-                qf[r][4 * c] = u.x;
-                qf[r][4 * c + 1] = u.y;
-                qf[r][4 * c + 2] = u.z;
-                qf[r][4 * c + 3] = u.w;
+            for (int st = 0; st < 4; ++st) {
+                uint4 u = make_uint4(0u, 0u, 0u, 0u);
+                if (head) u = *reinterpret_cast<const uint4*>(src + i16 * HD + (st >> 1) * 64 + g4 * 16 + (st & 1) * 8);
+                qm[st] = __builtin_bit_cast(bf16x8_t, u);
             }
+        } else {
+#pragma unroll
+            for (int r = 0; r < REP; ++r)
+#pragma unroll
+                for (int c = 0; c < E / 8; ++c) {
+                    const uint4 u = *reinterpret_cast<const uint4*>(src + r * HD + sub * E + 8 * c);
+                    qf[r][4 * c] = u.x;
+                    qf[r][4 * c + 1] = u.y;
+                    qf[r][4 * c + 2] = u.z;
+                    qf[r][4 * c + 3] = u.w;
+                }
+        }
     };
     // running max per key group; a finite floor so an all-masked group gives exp2(-inf) = 0
-    float m[REP], l[REP], acc[REP][E];
+    float m[MF ? 1 : REP], l[MF ? 1 : REP], acc[MF ? 1 : REP][E];
+    // MFMA path: softmax state of this lane's S^T column (one head), O rows of heads 4g..4g+3
+    float mm = kMinusHuge, lm = 0.f;
+    f32x4_t om[MF ? 8 : 1];                         // [j]: d = 8*i16 + j, rows = heads 4g..4g+3
     auto reset = [&]() {
+        if constexpr (MF) {
+            mm = kMinusHuge;
+            lm = 0.f;
 #pragma unroll
-        for (int r = 0; r < REP; ++r) {
-            m[r] = kMinusHuge;
-            l[r] = 0.f;
+            for (int j = 0; j < 8; ++j) om[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        } else {
 #pragma unroll
-            for (int e = 0; e < E; ++e) acc[r][e] = 0.f;
+            for (int r = 0; r < REP; ++r) {
+                m[r] = kMinusHuge;
+                l[r] = 0.f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) acc[r][e] = 0.f;
+            }
         }
     };
     auto compute = [&](const Piece& pc, int tile, const Tile& tl) {
         const int p0 = tile * kTileKeys;
+        if constexpr (MF) {
+            // S^T for keys kb*16 + 4g + r (rows) x heads (columns)
+            float sv[2][4];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const uint4 kw = tl.k[kb][st >> 1];
+                    const bf16x8_t ka = (st & 1) ? fp8x8_bf16(kw.z, kw.w) : fp8x8_bf16(kw.x, kw.y);
+                    sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qm[st], sa, 0, 0, 0);
+                }
+                const float ksr[4] = {row_bcast<0>(tl.ks[kb]), row_bcast<1>(tl.ks[kb]), row_bcast<2>(tl.ks[kb]),
+                                      row_bcast<3>(tl.ks[kb])};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool valid = p0 + kb * 16 + 4 * g4 + r < pc.kv_len;
+                    const float f = (SM == CVH_SCALE_PER_TOKEN_HEAD) ? ksr[r] * qsc : qsc;
+                    sv[kb][r] = valid ? sa[r] * f : -INFINITY;
+                }
+            }
+            float mt = fmaxf(fmaxf(fmaxf(sv[0][0], sv[0][1]), fmaxf(sv[0][2], sv[0][3])),
+                             fmaxf(fmaxf(sv[1][0], sv[1][1]), fmaxf(sv[1][2], sv[1][3])));
+            mt = xor32_max(xor16_max(mt));            // the column's (head's) tile max over the 4 lane groups
+            const bool need = mt > mm + kRescaleThreshold;
+            if (__builtin_amdgcn_ballot_w64(need) != 0) {
+                const float mn = need ? mt : mm;
+                const float c = __builtin_amdgcn_exp2f(mm - mn);
+                lm *= c;
+                mm = mn;
+                // O rows are heads 4g..4g+3: their factors live in the S^T columns (lanes) 4g + r
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float cr = __shfl(c, 4 * g4 + r, 64);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) om[j][r] *= cr;
+                }
+            }
+            uint32_t pw[4];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const float vsr[4] = {row_bcast<0>(tl.vs[kb]), row_bcast<1>(tl.vs[kb]), row_bcast<2>(tl.vs[kb]),
+                                      row_bcast<3>(tl.vs[kb])};
+#pragma unroll
+                for (int r = 0; r < 4; r += 2) {
+                    const float p0v = __builtin_amdgcn_exp2f(sv[kb][r] - mm);
+                    const float p1v = __builtin_amdgcn_exp2f(sv[kb][r + 1] - mm);
+                    lm += p0v + p1v;
+                    const float w0 = (SM == CVH_SCALE_PER_TOKEN_HEAD) ? p0v * vsr[r] : p0v;
+                    const float w1 = (SM == CVH_SCALE_PER_TOKEN_HEAD) ? p1v * vsr[r + 1] : p1v;
+                    pw[kb * 2 + r / 2] = pack_bf16x2_rne(w0, w1);
+                }
+            }
+            const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+#pragma unroll
+            for (int hw = 0; hw < 2; ++hw) {        // d = 8*i16 + 4*hw + jj
+                uint32_t t0[4], t1[4];
+                const uint32_t w0[4] = {hw ? tl.v[0][0].y : tl.v[0][0].x, hw ? tl.v[0][1].y : tl.v[0][1].x,
+                                        hw ? tl.v[0][2].y : tl.v[0][2].x, hw ? tl.v[0][3].y : tl.v[0][3].x};
+                const uint32_t w1[4] = {hw ? tl.v[1][0].y : tl.v[1][0].x, hw ? tl.v[1][1].y : tl.v[1][1].x,
+                                        hw ? tl.v[1][2].y : tl.v[1][2].x, hw ? tl.v[1][3].y : tl.v[1][3].x};
+                transpose4x4(w0, t0);               // t0[jj]: keys 4g..4g+3 at d = 8*i16 + 4*hw + jj
+                transpose4x4(w1, t1);               // t1[jj]: keys 16+4g..
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    om[4 * hw + jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, fp8x8_bf16(t0[jj], t1[jj]),
+                                                                            om[4 * hw + jj], 0, 0, 0);
+            }
+        } else {
         float sc[REP][kSteps];
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
@@ -686,6 +865,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 for (int e = 0; e < E; ++e) acc[r][e] += wgt * vf[e];
             }
         }
+        }
     };
     // End of a piece: combine the 8 key groups (rescale each to the wave max, then sum) and
     // write the finished row, or the partial of a cut row to slot 0 (holds u0) / 1 (holds u1-1).
@@ -701,6 +881,39 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const int v_own = (b4 ? 0 : NV / 2) + (b5 ? 0 : NV / 4) + (b3 ? NV8 : 0);   // first value index kept
     const int r_own = v_own / E, e_own = v_own % E;
     auto finish = [&](const Piece& pc) {
+        const int64_t pr0 = pfx(pc.row), pr1 = pfx(pc.row + 1);
+        if constexpr (MF) {
+            const float L = xor32_sum(xor16_sum(lm));   // the column's (head's) sum over all its keys
+            float Lr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Lr[r] = __shfl(L, 4 * g4 + r, 64);   // heads of this lane's O rows
+            if (pc.lt == 0 && pc.le == pr1 - pr0) {
+                const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int head = 4 * g4 + r;
+                    if (head >= REP) continue;
+                    const float f = vfin / Lr[r];
+                    uint16_t* o = p.out + ((int64_t)pc.t * H + pc.g * REP + head) * HD + 8 * i16;
+                    *reinterpret_cast<uint4*>(o) = make_uint4(pack_bf16x2_rne(om[0][r] * f, om[1][r] * f),
+                                                              pack_bf16x2_rne(om[2][r] * f, om[3][r] * f),
+                                                              pack_bf16x2_rne(om[4][r] * f, om[5][r] * f),
+                                                              pack_bf16x2_rne(om[6][r] * f, om[7][r] * f));
+                }
+            } else {
+                const int slot = (pr0 <= u0) ? 0 : 1;
+                const int64_t base = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int head = 4 * g4 + r;
+                    if (head >= REP) continue;
+                    float* pa = p.part_acc + (base + head) * HD + 8 * i16;
+                    *reinterpret_cast<float4*>(pa) = make_float4(om[0][r], om[1][r], om[2][r], om[3][r]);
+                    *reinterpret_cast<float4*>(pa + 4) = make_float4(om[4][r], om[5][r], om[6][r], om[7][r]);
+                }
+                if (g4 == 0 && i16 < REP) reinterpret_cast<float2*>(p.part_ml)[base + i16] = make_float2(mm, L);
+            }
+        } else {
         float cs[REP];
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
@@ -738,7 +951,6 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 l_own = l[r];
                 m_own = m[r];
             }
-        const int64_t pr0 = pfx(pc.row), pr1 = pfx(pc.row + 1);
         if (pc.lt == 0 && pc.le == pr1 - pr0) {
             const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
             const float f = vfin / l_own;
@@ -760,6 +972,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 #pragma unroll
             for (int i = 0; i < NV8; ++i) pa[i] = res[i];
             if (sub == 0 && e_own == 0) reinterpret_cast<float2*>(p.part_ml)[idx] = make_float2(m_own, l_own);
+        }
         }
     };
 
@@ -798,6 +1011,36 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             preQ = false;
             take_q(pa_);
             reset();
+            if constexpr (MF) {
+                // one tile in flight while one is computed (two register tiles): the MFMA tiles
+                // are larger than the VALU ones and three do not fit the register budget
+                for (;;) {
+                    compute(pa_, ta_, A);
+                    if (ta_ + 1 == pa_.le) {
+                        finish(pa_);
+                        if (pb_.row < 0) break;
+                        reset();
+                        take_q(pb_);
+                    }
+                    pa_ = lp;
+                    ta_ = lt;
+                    load_tile(pa_, ta_, A, ph, pa_.row >= 0);
+                    advance();
+                    ph = lookup(lp, lt);
+                    compute(pb_, tb_, B);
+                    if (tb_ + 1 == pb_.le) {
+                        finish(pb_);
+                        if (pa_.row < 0) break;
+                        reset();
+                        take_q(pa_);
+                    }
+                    pb_ = lp;
+                    tb_ = lt;
+                    load_tile(pb_, tb_, B, ph, pb_.row >= 0);
+                    advance();
+                    ph = lookup(lp, lt);
+                }
+            } else
             for (;;) {
                 pc_ = lp;
                 tc_ = lt;
@@ -872,10 +1115,11 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
     const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
     __shared__ float xs[6][512];
     const int half = static_cast<int>(blockDim.x) / 2, part = static_cast<int>(threadIdx.x) >= half ? 1 : 0;
-    const int ti = static_cast<int>(threadIdx.x) - part * half;
-    {
-        const int hh = ti / TPH;
-        const int d0 = (ti % TPH) * 4;
+    const int slices = heads_per_row * TPH;          // a multiple of half (half = min(512, slices))
+    for (int base = 0; base < slices; base += half) {
+        const int ti = static_cast<int>(threadIdx.x) - part * half;
+        const int hh = (base + ti) / TPH;
+        const int d0 = ((base + ti) % TPH) * 4;
         float M = kMinusHuge, L = 0.f;
         float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 4
@@ -899,8 +1143,7 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
             xs[0][ti] = M; xs[1][ti] = L; xs[2][ti] = A.x; xs[3][ti] = A.y; xs[4][ti] = A.z; xs[5][ti] = A.w;
         }
         __syncthreads();
-        if (part) return;
-        {
+        if (!part) {
             const float M1 = xs[0][ti], Mn = fmaxf(M, M1);
             const float c0 = exp2f(M - Mn), c1 = exp2f(M1 - Mn);
             L = L * c0 + xs[1][ti] * c1;
@@ -908,13 +1151,14 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
             A.y = A.y * c0 + xs[3][ti] * c1;
             A.z = A.z * c0 + xs[4][ti] * c1;
             A.w = A.w * c0 + xs[5][ti] * c1;
+            const float f = vfin / L;
+            const int h = hgi * heads_per_row + hh;      // query head index within the token
+            uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
+            const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
+            const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
+            *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
         }
-        const float f = vfin / L;
-        const int h = hgi * heads_per_row + hh;      // query head index within the token
-        uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
-        const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
-        const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
-        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
+        __syncthreads();                             // xs is reused by the next slice batch
     }
 }
 
@@ -1077,6 +1321,12 @@ bool launch_decode_rep(int rep, int G, int threads, size_t lds, hipStream_t s, c
     switch (rep) {
         case 1: launch_decode<HD, 1, SM>(G, threads, lds, s, p, one_block, planned); return true;
         case 2: launch_decode<HD, 2, SM>(G, threads, lds, s, p, one_block, planned); return true;
+        case 4:
+            if constexpr (HD == 128) { launch_decode<HD, 4, SM>(G, threads, lds, s, p, one_block, planned); return true; }
+            return false;
+        case 8:
+            if constexpr (HD == 128) { launch_decode<HD, 8, SM>(G, threads, lds, s, p, one_block, planned); return true; }
+            return false;
         default: return false;
     }
 }
@@ -1100,7 +1350,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     // that read the same K/V (consecutive, so in one workgroup, reading each tile together: the
     // second read hits the cache). One wave then holds two query heads' accumulators, as at GQA 2,
     // instead of spilling 4 or 8 heads' worth of registers.
-    const int kv_split = rep > 2 ? rep / 2 : 1;
+    const int kv_split = virtual_kv_split(rep, head_dim);
     const int kv_shift = kv_split == 4 ? 2 : kv_split == 2 ? 1 : 0;
     n_kv_heads *= kv_split;
     const int rep_v = rep / kv_split;
@@ -1142,7 +1392,14 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     p.n_kv = n_kv_heads;
     p.kv_shift = kv_shift;
     p.wpg = wpg;
-    p.qrows = q_stage_rows(wpg, rep_v, head_dim);
+    {
+        // q staging rows: as many as the LDS left by the row prefix and token table allows
+        const size_t fixed = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens));
+        const size_t per_row = static_cast<size_t>(wpg) * rep_v * head_dim * 2;
+        const int fit = fixed < kLdsBytes ? static_cast<int>((kLdsBytes - fixed) / per_row) : 0;
+        if (fit < 1) return CVH_ERR_UNSUPPORTED;
+        p.qrows = std::min(q_stage_rows(wpg, rep_v, head_dim), fit);
+    }
     p.log2_bs = lg;
     // The softmax scale is folded into q with log2(e) (base-2 softmax); a per-tensor K scale is a
     // device float, so the kernel folds it into q after reading it.
@@ -1177,8 +1434,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if ((phase & kPhaseMerge) && G > 1) {
         const dim3 mgrid(static_cast<unsigned>(rows));
         const int nt = static_cast<int>(num_tokens);
-        const int m2 = 2 * (wpg * rep_v * head_dim / 4);   // two halves, one thread per head slice
-        static_assert(8 * 2 * 128 / 4 <= 512, "wpg <= 8, rep_v <= 2, HD <= 128: one slice per thread");
+        // two halves of one thread per (head, 4 dims) slice, at most 512 each (more slices loop)
+        const int m2 = 2 * std::min(512, wpg * rep_v * head_dim / 4);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
@@ -1202,13 +1459,13 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
 }  // namespace
 }  // namespace cvh
 
-extern "C" int cvh_paged_attention_partitions(int64_t num_tokens, int n_heads, int n_kv_heads, int64_t table_width,
-                                              int block_size) {
+extern "C" int cvh_paged_attention_partitions(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                              int64_t table_width, int block_size) {
     if (num_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0 ||
         n_heads % n_kv_heads != 0)
         return 1;
     const int rep = n_heads / n_kv_heads;
-    const int n_kv = n_kv_heads * (rep > 2 ? rep / 2 : 1);   // the kernel's (virtual) kv heads, as in the launch
+    const int n_kv = n_kv_heads * cvh::virtual_kv_split(rep, head_dim);   // the kernel's kv heads, as in the launch
     return cvh::auto_partitions(num_tokens, n_kv, table_width, block_size);
 }
 
@@ -1218,7 +1475,7 @@ extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_
         partitions < 0 || n_heads % n_kv_heads != 0)
         return 0;
     const int rep = n_heads / n_kv_heads;
-    const int n_kv = n_kv_heads * (rep > 2 ? rep / 2 : 1);   // the kernel's (virtual) kv heads, as in the launch
+    const int n_kv = n_kv_heads * cvh::virtual_kv_split(rep, head_dim);   // the kernel's kv heads, as in the launch
     const int G = partitions ? partitions : cvh::auto_partitions(num_tokens, n_kv, table_width, block_size);
     return cvh::ws_layout(num_tokens, n_heads, n_kv, head_dim, G).total;
 }

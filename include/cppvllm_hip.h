@@ -60,9 +60,10 @@ enum { CVH_DTYPE_BF16 = 0, CVH_DTYPE_F16 = 1, CVH_DTYPE_F32 = 2 };
  *   token_kv_len int64 [num_tokens]  causal context length of each query token (positions+1);
  *                                    a token with kv_len <= 0 gets an all-zero output row
  *   scale        softmax scale (1/sqrt(head_dim) in the reference)
- * Supported: head_dim in {64,128}; n_heads/n_kv_heads in {1,2,4,8} (4 and 8 run as 2 and 4
- * virtual kv heads of 2 query heads per kv head, which halves / quarters the token limit below);
- * block_size a power of two in [16, 4096]; num_tokens <= 8192 for n_kv_heads <= 8
+ * Supported: head_dim in {64,128}; n_heads/n_kv_heads in {1,2,4,8} (at head_dim 128, 4 and 8 run
+ * on matrix cores with the query heads of a kv head as MFMA columns; at head_dim 64 they run as 2
+ * and 4 virtual kv heads of 2 query heads per kv head, which halves / quarters the token limit
+ * below); block_size a power of two in [16, 4096]; num_tokens <= 8192 for n_kv_heads <= 8
  * (num_tokens * n_kv_heads / 8 <= 8192 above): twice the reference engine's max_num_batched_tokens
  * (bench.cpp:25).
  * Queries of one sequence may be several tokens (chunked-prefill continuation).
@@ -203,8 +204,8 @@ size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int 
 
 /* The partition count the automatic policy picks for these shapes (the same count the launches
  * and cvh_paged_attention_workspace_bytes use for partitions = 0). */
-int cvh_paged_attention_partitions(int64_t num_tokens, int n_heads, int n_kv_heads, int64_t table_width,
-                                   int block_size);
+int cvh_paged_attention_partitions(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                   int64_t table_width, int block_size);
 
 /* ---------------------------------------------------------------------------------------------
  * RMSNorm family. Replaces fused::rms_norm / fused::add_rms_norm (kernels/fused_ops.h:7-9,

@@ -127,23 +127,52 @@ def test_max_rows_per_launch(orc):
     assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
 
 
-@pytest.mark.parametrize("H,limit", [(32, 4096), (64, 2048)])
-def test_virtual_head_row_limits(orc, H, limit):
-    """GQA 4 / 8 run as 2 / 4 virtual kv heads per kv head, so at 8 kv heads a launch takes at
-    most 4096 / 2048 query tokens: the limit itself is computed (sampled rows vs the oracle), one
-    token more is rejected with CVH_ERR_UNSUPPORTED before anything runs."""
-    say(f"virtual-head row limit H={H} T={limit}")
+@pytest.mark.parametrize("H,HD,limit", [(32, 64, 4096), (64, 64, 2048), (64, 128, 8192)])
+def test_gqa_row_limits(orc, H, HD, limit):
+    """At head_dim 64, GQA 4 / 8 run as 2 / 4 virtual kv heads per kv head, so at 8 kv heads a
+    launch takes at most 4096 / 2048 query tokens; at head_dim 128 they run on MFMA with one wave
+    per kv head and take the full 8192. The limit itself is computed (sampled rows vs the oracle),
+    one more token per sequence is rejected with CVH_ERR_UNSUPPORTED before anything runs."""
+    say(f"GQA row limit H={H} HD={HD} T={limit}")
     per = limit // 4
-    b = synth(43 + H, [per + 50, per + 300, per + 7, per + 999], 256, H=H, queries_per_seq=per)
+    b = synth(43 + H + HD, [per + 50, per + 300, per + 7, per + 999], 256, H=H, HD=HD, queries_per_seq=per)
     assert b["q"].shape[0] == limit
     got = run_gpu(dev(b))
-    rows = sorted(np.random.default_rng(H).choice(limit, 96, replace=False).tolist())
+    rows = sorted(np.random.default_rng(H + HD).choice(limit, 96, replace=False).tolist())
     assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
-    b1 = dev(synth(44 + H, [per + 50, per + 300, per + 7, per + 999], 256, H=H, queries_per_seq=per + 1))
+    b1 = dev(synth(44 + H + HD, [per + 50, per + 300, per + 7, per + 999], 256, H=H, HD=HD,
+                   queries_per_seq=per + 1))
     assert b1["q"].shape[0] == limit + 4
     with pytest.raises(_lib.CvhError) as err:
         run_gpu(b1)
     assert err.value.code == _lib.CVH_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("H", [32, 64])
+def test_gqa_mfma_config3_and_planned(orc, H):
+    """GQA 4 / 8 on the MFMA path at the headline shape (config-3 K/V, 256 sequences, 256-token
+    blocks): oracle parity on sampled rows, planned == unplanned bitwise, and every head equals
+    the same head computed by the GQA-2 (VALU) kernel: query heads 2i, 2i+1 of each kv head's
+    group go through a GQA-2 launch of their own, so two independent kernels agree on all rows."""
+    say(f"GQA MFMA config 3 H={H}")
+    b = workloads.config3(device="cpu")
+    g = torch.Generator().manual_seed(H)
+    rep = H // 8
+    b["n_heads"] = H
+    b["q"] = torch.randn((b["q"].shape[0], H, 128), generator=g).to(torch.bfloat16)
+    db = dev(b)
+    got = run_gpu(db)
+    rows = list(range(0, 256, 9))
+    assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
+    assert np.array_equal(run_planned(db), got)
+    q8 = db["q"].view(256, 8, rep, 128)
+    for i in range(rep // 2):
+        d2 = dict(db)
+        d2["n_heads"] = 16
+        d2["q"] = q8[:, :, 2 * i:2 * i + 2].reshape(256, 16, 128).contiguous()
+        two = run_gpu(d2).reshape(256, 8, 2, 128)
+        mine = got.reshape(256, 8, rep, 128)[:, :, 2 * i:2 * i + 2]
+        assert_close_bf16(mine, two, max_abs=1.6e-2, mean_abs=1e-3)
 
 
 def test_empty_context_rows_are_zero(orc):

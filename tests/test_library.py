@@ -118,7 +118,7 @@ def test_partition_policy_and_workspace_sizes():
     lib = _lib.lib()
     # headline decode (256 tokens, 8 kv heads = one 8-wave row group, 8 x 256-token blocks):
     # 256 partitions (2048 resident waves / 8)
-    assert lib.cvh_paged_attention_partitions(256, 16, 8, 8, 256) == 256
+    assert lib.cvh_paged_attention_partitions(256, 16, 8, 128, 8, 256) == 256
     rows, slots = 256, 256 * 2 * 16     # [G][2][WPG*REP] partial slots
     r256 = lambda v: (v + 255) // 256 * 256
     # plan: int2 token metadata [T] + int32 shared-prefix keys [T] + 184-byte workgroup records [G]
@@ -126,26 +126,34 @@ def test_partition_policy_and_workspace_sizes():
     want = r256((rows + 1) * 4) + r256(slots * 128 * 4) + r256(slots * 2 * 4) + r256(256 * 8) + r256(256 * 4) + \
         r256(256 * 184)
     assert lib.cvh_paged_attention_workspace_bytes(256, 16, 8, 128, 8, 256, 0) == want
-    # GQA 4 / 8 run as 2 / 4 virtual kv heads of 2 query heads per kv head: twice / four times the rows
-    # (prefix), the same partial slots per query head
+    # GQA 4 / 8 at head_dim 128 run on MFMA with one wave per physical kv head: the same 256 rows,
+    # partial slots for all H query heads of a row group
+    for H in (32, 64):
+        want_m = r256(257 * 4) + r256(256 * 2 * H * 128 * 4) + r256(256 * 2 * H * 2 * 4) + r256(256 * 8) + \
+            r256(256 * 4) + r256(256 * 184)
+        assert lib.cvh_paged_attention_workspace_bytes(256, H, 8, 128, 8, 256, 0) == want_m, H
+    # at head_dim 64 they run as 2 / 4 virtual kv heads of 2 query heads per kv head: twice / four
+    # times the rows (prefix), the same partial slots per query head
     for H, vrows in ((32, 512), (64, 1024)):
-        want_v = r256((vrows + 1) * 4) + r256(256 * 2 * H // (vrows // 256) * 128 * 4) + \
+        want_v = r256((vrows + 1) * 4) + r256(256 * 2 * H // (vrows // 256) * 64 * 4) + \
             r256(256 * 2 * H // (vrows // 256) * 2 * 4) + r256(256 * 8) + r256(256 * 4) + r256(256 * 184)
-        assert lib.cvh_paged_attention_workspace_bytes(256, H, 8, 128, 8, 256, 0) == want_v, H
+        assert lib.cvh_paged_attention_workspace_bytes(256, H, 8, 64, 8, 256, 0) == want_v, H
     # small batches: never less than two tiles per partition
-    assert lib.cvh_paged_attention_partitions(1, 1, 1, 1, 16) == 1
+    assert lib.cvh_paged_attention_partitions(1, 1, 1, 128, 1, 16) == 1
     # few rows: at most 8 partitions per row (8 rows -> 64, though 2 tiles each would allow 128)
-    assert lib.cvh_paged_attention_partitions(8, 16, 8, 4, 256) == 64
-    assert lib.cvh_paged_attention_partitions(16, 16, 8, 8, 256) == 128
+    assert lib.cvh_paged_attention_partitions(8, 16, 8, 128, 4, 256) == 64
+    assert lib.cvh_paged_attention_partitions(16, 16, 8, 128, 8, 256) == 128
     # one kv head: one-wave workgroups, capped at 1024 (not one per resident wave slot, 2048)
-    assert lib.cvh_paged_attention_partitions(256, 2, 1, 8, 256) == 1024
-    assert lib.cvh_paged_attention_partitions(256, 4, 2, 8, 256) == 1024
-    # GQA 4: the policy sees the launch's virtual kv heads (16 = 2 row groups per token), so 16
-    # tokens give 32 rows and up to 8 partitions each: 256, as the launch and workspace size use
-    assert lib.cvh_paged_attention_partitions(16, 32, 8, 8, 256) == 256
-    r16 = r256(33 * 4) + r256(256 * 2 * 16 * 128 * 4) + r256(256 * 2 * 16 * 2 * 4) + r256(16 * 8) + \
+    assert lib.cvh_paged_attention_partitions(256, 2, 1, 128, 8, 256) == 1024
+    assert lib.cvh_paged_attention_partitions(256, 4, 2, 128, 8, 256) == 1024
+    # GQA 4 at head_dim 64: the policy sees the launch's virtual kv heads (16 = 2 row groups per
+    # token), so 16 tokens give 32 rows and up to 8 partitions each: 256, as the launch and the
+    # workspace size use; at head_dim 128 (MFMA, 16 rows): 128
+    assert lib.cvh_paged_attention_partitions(16, 32, 8, 64, 8, 256) == 256
+    r16 = r256(33 * 4) + r256(256 * 2 * 16 * 64 * 4) + r256(256 * 2 * 16 * 2 * 4) + r256(16 * 8) + \
         r256(16 * 4) + r256(256 * 184)
-    assert lib.cvh_paged_attention_workspace_bytes(16, 32, 8, 128, 8, 256, 0) == r16
+    assert lib.cvh_paged_attention_workspace_bytes(16, 32, 8, 64, 8, 256, 0) == r16
+    assert lib.cvh_paged_attention_partitions(16, 32, 8, 128, 8, 256) == 128
     assert lib.cvh_paged_attention_workspace_bytes(4, 16, 8, 128, 8, 16, -1) == 0
 
 
