@@ -73,6 +73,8 @@ def cpu_baseline(b, reps: int = 5):
     med = statistics.median(times)
     nbytes = workloads.attention_bytes(args[7].tolist(), n_kv=KV, n_heads=H)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "omp_max_threads": oracle.max_threads(),
             "sample": f"one layer of config 3 (all 256 tokens, {nbytes / 1e6:.1f} MB algorithmic), "
                       f"median of {reps} after 1 warm-up: {med * 1e3:.1f} ms/layer"}
 
