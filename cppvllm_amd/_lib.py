@@ -72,6 +72,12 @@ SIGNATURES = {
     "cvh_gemm_bf16_nt_swiglu": (i32, [vp, vp, vp, i64, i32, i32, i32, vp]),
     "cvh_gemm_bf16_nt_swiglu_config": (i32, [i64, i32, i32]),
     "cvh_gemm_bf16_nt_swiglu_configs": (i32, [vp, i32]),
+    "cvh_gemm_bf16_nt_residual": (i32, [vp, vp, vp, vp, i64, i32, i32, i32, vp]),
+    "cvh_gemm_bf16_nt_swiglu_rownorm": (i32, [vp, vp, vp, f64, vp, i64, i32, i32, i32, vp]),
+    "cvh_gemm_qkv_norm_rope_kv_write_fp8": (i32, [vp, vp, vp, f64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64,
+                                                  i32, i32, i32, i32, i32, i32, f64, i32, vp]),
+    "cvh_gemm_fused_configs": (i32, [i32, vp, i32]),
+    "cvh_gemm_fused_config": (i32, [i32, i64]),
     "cvh_version": (C.c_char_p, []),
 }
 

@@ -78,24 +78,10 @@ template <> struct Chunk8<float> {
     }
 };
 
-// How a row's input x is read: plainly, or with agent-scope coherent loads (relaxed atomics, the
-// sc1 bit) when another workgroup of the same kernel wrote it (see the GEMM's fused norm).
+// Plain 16-byte row loads for norm_row.
 struct PlainChunk {
     template <typename T>
     __device__ __forceinline__ void operator()(const T* p, T (&v)[8]) const { Chunk8<T>::load(p, v); }
-};
-struct AgentChunk {
-    __device__ __forceinline__ void operator()(const uint16_t* p, uint16_t (&v)[8]) const {
-        const uint64_t a = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t b = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p) + 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            v[i] = static_cast<uint16_t>(a >> (16 * i));
-            v[4 + i] = static_cast<uint16_t>(b >> (16 * i));
-        }
-    }
 };
 
 // ---- DPP helpers (within rows of 16 lanes) ---------------------------------------------------
@@ -247,5 +233,172 @@ __device__ __forceinline__ void fp8x4_to_f32(uint32_t w, float* f) {
 }
 
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// ---- QK-RMSNorm + neox RoPE + FP8 K/V write of one (token, head) task -----------------------
+// Task order in a token's packed qkv row: H query heads, KV key heads, KV value heads
+// (kernels/fused_ops.cu:118-122). A task runs on 16 lanes; lane gl owns elements [P*gl, P*gl+P) and
+// [HALF+P*gl, HALF+P*gl+P), P = HD/32, so the neox pair (e, e+HALF) sits in one lane. The load
+// phases request the task's inputs (head values; norm gains and this position's cos/sin), the run
+// phase does the arithmetic, so a caller can issue the loads early or overlap several tasks. Shared by the
+// standalone kernel and the QKV-projection epilogue, which must agree bit for bit; callers are
+// built without FMA contraction.
+struct QkvDst {
+    uint16_t* q_out;
+    const uint16_t* q_norm;
+    const uint16_t* k_norm;
+    const float* cos_t;
+    const float* sin_t;
+    uint8_t* k_cache;
+    uint8_t* v_cache;
+    float* k_scale;
+    float* v_scale;
+    uint16_t* k_dense;
+    uint16_t* v_dense;
+    int H, KV, log2_bs;
+    float eps;
+};
+
+template <int HD>
+struct QkvTaskIn {
+    static constexpr int P = HD / 32;
+    float x[2 * P], wv[2 * P], cs[P], sn[P];
+};
+
+// The head's HD bf16 values (src: global or LDS).
+template <int HD>
+__device__ __forceinline__ void qkv_task_load_x(QkvTaskIn<HD>& in, const uint16_t* src, int gl) {
+    constexpr int HALF = HD / 2, P = HD / 32;
+    const int e0 = P * gl;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        in.x[j] = bf16_bits_to_f32(src[e0 + j]);
+        in.x[P + j] = bf16_bits_to_f32(src[HALF + e0 + j]);
+    }
+}
+// Q/K tasks: the norm gains and this position's cos/sin.
+template <int HD>
+__device__ __forceinline__ void qkv_task_load_consts(QkvTaskIn<HD>& in, int task, int64_t pos, const QkvDst& d,
+                                                     int gl) {
+    constexpr int HALF = HD / 2, P = HD / 32;
+    const int e0 = P * gl;
+    if (task < d.H + d.KV) {
+        const uint16_t* wn = task < d.H ? d.q_norm : d.k_norm;
+        const float* cr = d.cos_t + pos * HALF + e0;
+        const float* sr = d.sin_t + pos * HALF + e0;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            in.wv[j] = bf16_bits_to_f32(wn[e0 + j]);
+            in.wv[P + j] = bf16_bits_to_f32(wn[HALF + e0 + j]);
+            in.cs[j] = cr[j];
+            in.sn[j] = sr[j];
+        }
+    }
+}
+
+template <int HD, int SCALE_MODE>
+__device__ __forceinline__ void qkv_task_run(const QkvTaskIn<HD>& in, int64_t t, int task, int64_t slot,
+                                             const QkvDst& d, int gl) {
+    constexpr int HALF = HD / 2, P = HD / 32;
+    const int e0 = P * gl;
+    const int H = d.H, KV = d.KV;
+    const int bs_mask = (1 << d.log2_bs) - 1;
+    if (task >= H + KV) {                // ---- V: quantise (kernels/fused_ops.cu:125-143)
+        const int kvh = task - H - KV;
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2 * P; ++j) amax = fmaxf(amax, fabsf(in.x[j]));
+        amax = xor_max<16>(amax);
+        if (d.v_dense != nullptr) {
+            uint16_t* o = d.v_dense + (t * KV + kvh) * HD;
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                o[e0 + j] = static_cast<uint16_t>(__float_as_uint(in.x[j]) >> 16);   // the input bits
+                o[HALF + e0 + j] = static_cast<uint16_t>(__float_as_uint(in.x[P + j]) >> 16);
+            }
+        }
+        if (slot < 0) return;
+        float sc, inv;
+        if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
+            sc = fmaxf(amax, 1e-8f) / 448.0f;
+            inv = 1.0f / sc;
+        } else {
+            inv = 1.0f / d.v_scale[0];
+        }
+        uint8_t* dst = d.v_cache + (slot * KV + kvh) * HD;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            dst[e0 + j] = static_cast<uint8_t>(e4m3_encode(in.x[j] * inv));
+            dst[HALF + e0 + j] = static_cast<uint8_t>(e4m3_encode(in.x[P + j] * inv));
+        }
+        if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
+            if (gl == 0) d.v_scale[(((slot >> d.log2_bs) * KV + kvh) << d.log2_bs) + (slot & bs_mask)] = sc;
+        }
+        return;
+    }
+
+    // ---- Q / K: per-head RMSNorm (kernels/fused_ops.cu:145-156)
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2 * P; ++j) ss = ss + in.x[j] * in.x[j];
+    ss = xor_sum<16>(ss);
+    const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(HD) + d.eps);
+    float n[2 * P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        n[j] = round_bf16(round_bf16(in.x[j] * inv) * in.wv[j]);
+        n[P + j] = round_bf16(round_bf16(in.x[P + j] * inv) * in.wv[P + j]);
+    }
+    // ---- neox RoPE on (e, e+HALF) (kernels/fused_ops.cu:157-166)
+    float r[2 * P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        const float c = in.cs[j], s = in.sn[j];
+        const float a = n[j], b = n[P + j];
+        const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+        r[j] = ac - bs;
+        r[P + j] = bc + as;
+    }
+    if (task < H) {                      // (kernels/fused_ops.cu:168-173)
+        uint16_t* dst = d.q_out + (t * H + task) * HD;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            dst[e0 + j] = f32_to_bf16_bits(r[j]);
+            dst[HALF + e0 + j] = f32_to_bf16_bits(r[P + j]);
+        }
+        return;
+    }
+
+    // ---- K: round to bf16, amax scale, e4m3 (kernels/fused_ops.cu:175-190)
+    const int kvh = task - H;
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2 * P; ++j) { r[j] = round_bf16(r[j]); amax = fmaxf(amax, fabsf(r[j])); }
+    amax = xor_max<16>(amax);
+    if (d.k_dense != nullptr) {
+        uint16_t* o = d.k_dense + (t * KV + kvh) * HD;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            o[e0 + j] = f32_to_bf16_bits(r[j]);
+            o[HALF + e0 + j] = f32_to_bf16_bits(r[P + j]);
+        }
+    }
+    if (slot < 0) return;
+    float sc, sinv;
+    if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
+        sc = fmaxf(amax, 1e-8f) / 448.0f;
+        sinv = 1.0f / sc;
+    } else {
+        sinv = 1.0f / d.k_scale[0];
+    }
+    uint8_t* dst = d.k_cache + (slot * KV + kvh) * HD;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        dst[e0 + j] = static_cast<uint8_t>(e4m3_encode(r[j] * sinv));
+        dst[HALF + e0 + j] = static_cast<uint8_t>(e4m3_encode(r[P + j] * sinv));
+    }
+    if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
+        if (gl == 0) d.k_scale[(((slot >> d.log2_bs) * KV + kvh) << d.log2_bs) + (slot & bs_mask)] = sc;
+    }
+}
 
 }  // namespace cvh

@@ -34,151 +34,27 @@ __global__ __launch_bounds__(64 * kNormWaves) void rms_norm_kernel(typename Elem
 }
 
 // ---- QK-RMSNorm + RoPE + FP8 KV write --------------------------------------------------------
-// One 16-lane group per (token, head task); task order inside a token row follows the packed
-// qkv layout: H query heads, KV key heads, KV value heads (kernels/fused_ops.cu:118-122).
-// Lane i of a group owns elements [P*i, P*i+P) and [HALF+P*i, HALF+P*i+P), P = HD/32, so the
-// neox RoPE pair (e, e+HALF) lives in one lane and needs no cross-lane exchange.
+// One 16-lane group per (token, head task), the task body shared with the QKV-projection epilogue
+// (qkv_task_load / qkv_task_run).
 constexpr int kQkvGroupsPerBlock = 16;   // 256 threads
 
 template <int HD, int SCALE_MODE>
-__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
-        uint16_t* __restrict__ q_out, const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ q_norm,
-        const uint16_t* __restrict__ k_norm, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-        const int64_t* __restrict__ positions, const int64_t* __restrict__ slots, uint8_t* __restrict__ k_cache,
-        uint8_t* __restrict__ v_cache, float* __restrict__ k_scale, float* __restrict__ v_scale,
-        uint16_t* __restrict__ k_dense, uint16_t* __restrict__ v_dense, int H, int KV, int log2_bs, float eps) {
-    constexpr int HALF = HD / 2;
-    constexpr int P = HD / 32;           // elements per lane per half (4 for HD=128, 2 for HD=64)
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(const uint16_t* __restrict__ qkv,
+                                                              const int64_t* __restrict__ positions,
+                                                              const int64_t* __restrict__ slots, QkvDst d) {
     const int gl = threadIdx.x & 15;     // lane inside the 16-lane group
-    const int n_tasks = H + 2 * KV;
+    const int n_tasks = d.H + 2 * d.KV;
     const int task = blockIdx.x * kQkvGroupsPerBlock + (threadIdx.x >> 4);
     if (task >= n_tasks) return;         // whole 16-lane groups exit together
     const int64_t t = blockIdx.y;
-    const uint16_t* src = qkv + (t * n_tasks + task) * HD;
-    const int e0 = P * gl;               // first-half element index; partner is e0 + HALF
-
     // every global input of the task is requested before the first reduction, so the kernel waits
-    // for memory once: the head, and for Q/K the norm gains and this position's cos/sin
+    // for memory once
     const int64_t slot = slots[t];
     const int64_t pos = positions[t];
-    const bool is_qk = task < H + KV;
-    float x[2 * P], wv[2 * P], cs[P], sn[P];
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-        x[j] = bf16_bits_to_f32(src[e0 + j]);
-        x[P + j] = bf16_bits_to_f32(src[HALF + e0 + j]);
-    }
-    if (is_qk) {
-        const uint16_t* wn = task < H ? q_norm : k_norm;
-        const float* cr = cos_t + pos * HALF + e0;
-        const float* sr = sin_t + pos * HALF + e0;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            wv[j] = bf16_bits_to_f32(wn[e0 + j]);
-            wv[P + j] = bf16_bits_to_f32(wn[HALF + e0 + j]);
-            cs[j] = cr[j];
-            sn[j] = sr[j];
-        }
-    }
-    const int bs_mask = (1 << log2_bs) - 1;
-
-    if (!is_qk) {                        // ---- V: quantise (kernels/fused_ops.cu:125-143)
-        const int kvh = task - H - KV;
-        float amax = 0.f;
-#pragma unroll
-        for (int j = 0; j < 2 * P; ++j) amax = fmaxf(amax, fabsf(x[j]));
-        amax = xor_max<16>(amax);
-        if (v_dense != nullptr) {
-            uint16_t* d = v_dense + (t * KV + kvh) * HD;
-#pragma unroll
-            for (int j = 0; j < P; ++j) { d[e0 + j] = src[e0 + j]; d[HALF + e0 + j] = src[HALF + e0 + j]; }
-        }
-        if (slot < 0) return;
-        float sc, inv;
-        if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
-            sc = fmaxf(amax, 1e-8f) / 448.0f;
-            inv = 1.0f / sc;
-        } else {
-            inv = 1.0f / v_scale[0];
-        }
-        uint8_t* dst = v_cache + (slot * KV + kvh) * HD;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            dst[e0 + j] = static_cast<uint8_t>(e4m3_encode(x[j] * inv));
-            dst[HALF + e0 + j] = static_cast<uint8_t>(e4m3_encode(x[P + j] * inv));
-        }
-        if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
-            if (gl == 0) v_scale[(((slot >> log2_bs) * KV + kvh) << log2_bs) + (slot & bs_mask)] = sc;
-        }
-        return;
-    }
-
-    // ---- Q / K: per-head RMSNorm (kernels/fused_ops.cu:145-156)
-    const bool is_q = task < H;
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 2 * P; ++j) ss = ss + x[j] * x[j];
-    ss = xor_sum<16>(ss);
-    const float inv = 1.0f / __builtin_sqrtf(ss / static_cast<float>(HD) + eps);
-
-    float n[2 * P];
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-        n[j] = round_bf16(round_bf16(x[j] * inv) * wv[j]);
-        n[P + j] = round_bf16(round_bf16(x[P + j] * inv) * wv[P + j]);
-    }
-    // ---- neox RoPE on (e, e+HALF) (kernels/fused_ops.cu:157-166)
-    float r[2 * P];
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-        const float c = cs[j], s = sn[j];
-        const float a = n[j], b = n[P + j];
-        const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
-        r[j] = ac - bs;
-        r[P + j] = bc + as;
-    }
-
-    if (is_q) {                          // (kernels/fused_ops.cu:168-173)
-        uint16_t* dst = q_out + (t * H + task) * HD;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            dst[e0 + j] = f32_to_bf16_bits(r[j]);
-            dst[HALF + e0 + j] = f32_to_bf16_bits(r[P + j]);
-        }
-        return;
-    }
-
-    // ---- K: round to bf16, amax scale, e4m3 (kernels/fused_ops.cu:175-190)
-    const int kvh = task - H;
-    float amax = 0.f;
-#pragma unroll
-    for (int j = 0; j < 2 * P; ++j) { r[j] = round_bf16(r[j]); amax = fmaxf(amax, fabsf(r[j])); }
-    amax = xor_max<16>(amax);
-    if (k_dense != nullptr) {
-        uint16_t* d = k_dense + (t * KV + kvh) * HD;
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            d[e0 + j] = f32_to_bf16_bits(r[j]);
-            d[HALF + e0 + j] = f32_to_bf16_bits(r[P + j]);
-        }
-    }
-    if (slot < 0) return;
-    float sc, sinv;
-    if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
-        sc = fmaxf(amax, 1e-8f) / 448.0f;
-        sinv = 1.0f / sc;
-    } else {
-        sinv = 1.0f / k_scale[0];
-    }
-    uint8_t* dst = k_cache + (slot * KV + kvh) * HD;
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-        dst[e0 + j] = static_cast<uint8_t>(e4m3_encode(r[j] * sinv));
-        dst[HALF + e0 + j] = static_cast<uint8_t>(e4m3_encode(r[P + j] * sinv));
-    }
-    if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
-        if (gl == 0) k_scale[(((slot >> log2_bs) * KV + kvh) << log2_bs) + (slot & bs_mask)] = sc;
-    }
+    QkvTaskIn<HD> in;
+    qkv_task_load_x<HD>(in, qkv + (t * n_tasks + task) * HD, gl);
+    qkv_task_load_consts<HD>(in, task, pos, d, gl);
+    qkv_task_run<HD, SCALE_MODE>(in, t, task, slot, d, gl);
 }
 
 __global__ __launch_bounds__(256) void e4m3_quantize_kernel(uint8_t* __restrict__ dst, const float* __restrict__ src,
@@ -270,15 +146,11 @@ extern "C" int cvh_qk_norm_rope_kv_write_fp8(void* q_out, const void* qkv, const
                     static_cast<unsigned>(num_tokens));
     auto s = reinterpret_cast<hipStream_t>(stream);
     const float e = static_cast<float>(eps);
-    auto* qo = static_cast<uint16_t*>(q_out);
+    const QkvDst d{static_cast<uint16_t*>(q_out), static_cast<const uint16_t*>(q_norm),
+                   static_cast<const uint16_t*>(k_norm), cos_t, sin_t, k_cache, v_cache, k_scale, v_scale,
+                   static_cast<uint16_t*>(k_dense), static_cast<uint16_t*>(v_dense), n_heads, n_kv_heads, lg, e};
     auto* in = static_cast<const uint16_t*>(qkv);
-    auto* qn = static_cast<const uint16_t*>(q_norm);
-    auto* kn = static_cast<const uint16_t*>(k_norm);
-    auto* kd = static_cast<uint16_t*>(k_dense);
-    auto* vd = static_cast<uint16_t*>(v_dense);
-#define CVH_QKV_LAUNCH(HD, SM)                                                                                       \
-    qk_norm_rope_kv_kernel<HD, SM><<<grid, 256, 0, s>>>(qo, in, qn, kn, cos_t, sin_t, positions, slots, k_cache,     \
-                                                        v_cache, k_scale, v_scale, kd, vd, n_heads, n_kv_heads, lg, e)
+#define CVH_QKV_LAUNCH(HD, SM) qk_norm_rope_kv_kernel<HD, SM><<<grid, 256, 0, s>>>(in, positions, slots, d)
     if (head_dim == 128) {
         if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD) CVH_QKV_LAUNCH(128, CVH_SCALE_PER_TOKEN_HEAD);
         else CVH_QKV_LAUNCH(128, CVH_SCALE_PER_TENSOR);

@@ -461,23 +461,38 @@ __device__ __forceinline__ void tile_epilogue(const f32x4_t (&acc)[MF][NF], uint
 }
 
 
-template <int MF, int NF, int WM, int WN, int S, int EPI = kEpiStore>
-__global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
-                                                         const uint16_t* __restrict__ w, int M, int N, int K) {
+// Shape constants of a tiled configuration.
+template <int MF, int NF, int WM, int WN, int S>
+struct Tiled {
     static_assert(WM * WN == 4, "four waves");
-    constexpr int BM = 16 * MF * WM, BN = 16 * NF * WN;
-    constexpr int kRowBytes = kChunk * 2;                       // 256 B per row chunk
-    constexpr int kStageBytes = (BM + BN) * kRowBytes;
-    constexpr int kDma = (BM + BN) * 16 / 256;                  // 16-byte DMA slots per thread per stage
+    static constexpr int BM = 16 * MF * WM, BN = 16 * NF * WN;
+    static constexpr int kRowBytes = kChunk * 2;                       // 256 B per row chunk
+    static constexpr int kStageBytes = (BM + BN) * kRowBytes;
+    static constexpr int kDma = (BM + BN) * 16 / 256;                  // 16-byte DMA slots per thread per stage
     static_assert((BM + BN) * 16 % 256 == 0, "whole DMA rounds");
-    constexpr int kStages = S > 0 ? S : stages_for(kStageBytes, kDma);   // S = 0: as deep as fits
+    static constexpr int kStages = S > 0 ? S : stages_for(kStageBytes, kDma);   // S = 0: as deep as fits
     static_assert(kStages >= 2 && kDma * (kStages - 2) <= 63 && kStages * kStageBytes <= 160 * 1024, "stages");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageBytes];
+    static constexpr int kLdsBytes = kStages * kStageBytes;
+};
 
+// The K loop of a tiled workgroup: the BM x BN output tile at (m0, n0) accumulated in acc (wave
+// (wm, wn) holds MF x NF fragments). lds holds Tiled::kLdsBytes.
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+// hook() runs once, after the first chunk has landed (inputs requested before the loop have
+// arrived by then): an epilogue issues its dependent loads there so they land under the loop.
+template <int MF, int NF, int WM, int WN, int S, typename Hook = NoHook>
+__device__ __forceinline__ void tiled_mainloop(f32x4_t (&acc)[MF][NF], uint8_t* lds, const uint16_t* __restrict__ x,
+                                               const uint16_t* __restrict__ w, int M, int K, int m0, int n0,
+                                               Hook hook = Hook{}) {
+    using C = Tiled<MF, NF, WM, WN, S>;
+    constexpr int BM = C::BM, kRowBytes = C::kRowBytes, kStageBytes = C::kStageBytes, kDma = C::kDma;
+    constexpr int kStages = C::kStages;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int i16 = lane & 15, g = lane >> 4;
     const int wm = wave / WN, wn = wave % WN;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const uint32_t lds0 = lds_addr(lds);
 
     // this thread's DMA sources: slot L = (j*4 + wave)*64 + lane of a stage; rows [0, BM) are X,
@@ -498,7 +513,6 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ 
             dma16(src[j] + c * kChunk, __builtin_amdgcn_readfirstlane(base + (j * 4 + wave) * 1024));
     };
 
-    f32x4_t acc[MF][NF];
 #pragma unroll
     for (int f = 0; f < MF; ++f)
 #pragma unroll
@@ -513,10 +527,201 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ 
         __builtin_amdgcn_s_barrier();               // chunk c landed for every wave; stage of c-1 free
         asm volatile("" ::: "memory");
         if (c + kStages - 1 < nc) issue(c + kStages - 1, (c + kStages - 1) % kStages);
+        if (c == 0) hook();
         const uint8_t* st = lds + (c % kStages) * kStageBytes;
         chunk_mma<MF, NF>(acc, st + (wm * MF * 16) * kRowBytes, st + (BM + wn * NF * 16) * kRowBytes, i16, g);
     }
-    tile_epilogue<MF, NF, WN, EPI>(acc, y, M, N, m0, n0, wm, wn, i16, g);
+}
+
+template <int MF, int NF, int WM, int WN, int S, int EPI = kEpiStore>
+__global__ __launch_bounds__(256) void gemm_tiled_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w, int M, int N, int K) {
+    using C = Tiled<MF, NF, WM, WN, S>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[C::kLdsBytes];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int m0 = blockIdx.y * C::BM, n0 = blockIdx.x * C::BN;
+    f32x4_t acc[MF][NF];
+    tiled_mainloop<MF, NF, WM, WN, S>(acc, lds, x, w, M, K, m0, n0);
+    tile_epilogue<MF, NF, WN, EPI>(acc, y, M, N, m0, n0, wave / WN, wave % WN, lane & 15, lane >> 4);
+}
+
+// ---- tiled kernel with fused epilogues (the decode step's layer boundaries) ------------------
+// kEpiResid (o_proj, down_proj): resid <- rnd(resid + rnd(x.w^T)), the residual add of
+//   add_rms_norm (kernels/fused_ops.cu:70-73), and row_ss[m][n/16] <- the sum of squares of the
+//   new residual over the 16 columns n .. n+15 (in column order, then lanes 4g combined by xor 16,
+//   32), so the norm's sum over a row is the in-order sum of N/16 partials, whatever the tiling.
+// RS (qkv, gate/up after such a producer): x rows are the raw residual v; the row's RMS factor
+//   inv = 1 / sqrt(sum(row_ss) / K + eps) multiplies the accumulator before the epilogue's first
+//   rounding, and the norm gain is pre-multiplied into the weight columns, so y = rnd(inv * v.w'^T)
+//   with w' = rnd(w * gain) stands for rnd(rnd(rnd(v * inv) * gain) . w^T).
+// kEpiQkv (qkv projection): the bf16 tile goes to LDS and every (row, head) of it runs the QK-norm
+//   / RoPE / FP8 K/V write task (qkv_task_*) of the standalone kernel; BN is a whole number of
+//   128-wide heads, so a tile holds complete heads.
+enum { kEpiResid = 2, kEpiQkv = 3 };
+
+struct FusedArgs {
+    uint16_t* y;                 // kEpiStore: y [M][N]; kEpiSwiglu: act [M][N/2]; kEpiResid: resid [M][N]
+    float* ss_out;               // kEpiResid: [M][N/16]
+    const float* ss_in;          // RS: [M][K/16]
+    float eps_in;                // RS: the row norm's eps
+    const int64_t* positions;    // kEpiQkv
+    const int64_t* slots;        // kEpiQkv
+    QkvDst qkv;                  // kEpiQkv
+};
+
+constexpr int kMaxRsQuads = 4;   // RS: K / 256 float4 partial loads per lane (K <= 1024)
+
+template <int MF, int NF, int WM, int WN, int S, int EPI, bool RS, int SM>
+__global__ __launch_bounds__(256) void gemm_fused_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w, int M, int N, int K,
+                                                         FusedArgs a) {
+    using C = Tiled<MF, NF, WM, WN, S>;
+    constexpr int BM = C::BM, BN = C::BN;
+    constexpr int kTs = BN + 8;                                   // bf16 per LDS row of the kEpiQkv tile
+    constexpr int kEpiLds = EPI == kEpiQkv ? BM * kTs * 2 : 0;
+    constexpr int kLds = C::kLdsBytes > kEpiLds ? C::kLdsBytes : kEpiLds;
+    constexpr int kHeads = BN / 128;                              // kEpiQkv: heads per tile
+    constexpr int kTasks = BM * kHeads;
+    constexpr int kIter = (kTasks + 15) / 16;                     // tasks per 16-lane group
+    static_assert(EPI != kEpiQkv || BN % 128 == 0, "whole heads per tile");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    // Everything the epilogue reads from global memory is requested before the K loop's DMA (the
+    // loop's own vmcnt waits then cover it too).
+    float4 rsq[RS ? MF : 1][RS ? kMaxRsQuads : 1];
+    if constexpr (RS) {
+        const int nq = K >> 8;                                    // float4 per lane per row
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int m = min(m0 + (wm * MF + f) * 16 + i16, M - 1);
+            const float4* p = reinterpret_cast<const float4*>(a.ss_in + static_cast<size_t>(m) * (K >> 4)) + g * nq;
+#pragma unroll
+            for (int q = 0; q < kMaxRsQuads; ++q) rsq[f][q] = q < nq ? p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    uint2 hres[EPI == kEpiResid ? MF : 1][EPI == kEpiResid ? NF : 1];
+    if constexpr (EPI == kEpiResid) {
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int m = min(m0 + (wm * MF + f) * 16 + i16, M - 1);
+#pragma unroll
+            for (int e = 0; e < NF; ++e)
+                hres[f][e] = *reinterpret_cast<const uint2*>(a.y + static_cast<size_t>(m) * N + n0 +
+                                                             (wn * NF + e) * 16 + 4 * g);
+        }
+    }
+    int64_t tpos[EPI == kEpiQkv ? kIter : 1], tslot[EPI == kEpiQkv ? kIter : 1];
+    if constexpr (EPI == kEpiQkv) {
+#pragma unroll
+        for (int it = 0; it < kIter; ++it) {
+            const int r = (it * 16 + (static_cast<int>(threadIdx.x) >> 4)) / kHeads;
+            const int m = min(m0 + min(r, BM - 1), M - 1);
+            tpos[it] = a.positions[m];
+            tslot[it] = a.slots[m];
+        }
+    }
+
+    // kEpiQkv: the Q/K tasks' norm gains and cos/sin (which need the positions) are requested
+    // inside the K loop
+    QkvTaskIn<128> in[EPI == kEpiQkv ? kIter : 1];
+    const int gl = threadIdx.x & 15, grp = threadIdx.x >> 4;
+    auto hook = [&]() {
+        if constexpr (EPI == kEpiQkv) {
+#pragma unroll
+            for (int it = 0; it < kIter; ++it)
+                qkv_task_load_consts<128>(in[it], n0 / 128 + (it * 16 + grp) % kHeads, tpos[it], a.qkv, gl);
+        }
+    };
+    f32x4_t acc[MF][NF];
+    tiled_mainloop<MF, NF, WM, WN, S>(acc, lds, x, w, M, K, m0, n0, hook);
+
+    if constexpr (RS) {
+        const int nq = K >> 8;
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            float sum = 0.f;
+#pragma unroll
+            for (int q = 0; q < kMaxRsQuads; ++q) {
+                if (q < nq) {
+                    sum = sum + rsq[f][q].x;
+                    sum = sum + rsq[f][q].y;
+                    sum = sum + rsq[f][q].z;
+                    sum = sum + rsq[f][q].w;
+                }
+            }
+            sum = sum + shfl_xor(sum, 16);
+            sum = sum + shfl_xor(sum, 32);
+            const float inv = 1.0f / __builtin_sqrtf(sum / static_cast<float>(K) + a.eps_in);
+#pragma unroll
+            for (int e = 0; e < NF; ++e) acc[f][e] *= inv;
+        }
+    }
+
+    if constexpr (EPI == kEpiStore || EPI == kEpiSwiglu) {
+        tile_epilogue<MF, NF, WN, EPI>(acc, a.y, M, N, m0, n0, wm, wn, i16, g);
+    } else if constexpr (EPI == kEpiResid) {
+        const int nss = N >> 4;
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int m = m0 + (wm * MF + f) * 16 + i16;
+#pragma unroll
+            for (int e = 0; e < NF; ++e) {
+                const uint32_t y01 = pack_bf16x2(acc[f][e][0], acc[f][e][1]);
+                const uint32_t y23 = pack_bf16x2(acc[f][e][2], acc[f][e][3]);
+                const float yv[4] = {bf16_bits_to_f32(y01 & 0xffffu), bf16_bits_to_f32(y01 >> 16),
+                                     bf16_bits_to_f32(y23 & 0xffffu), bf16_bits_to_f32(y23 >> 16)};
+                const float hv[4] = {bf16_bits_to_f32(hres[f][e].x & 0xffffu), bf16_bits_to_f32(hres[f][e].x >> 16),
+                                     bf16_bits_to_f32(hres[f][e].y & 0xffffu), bf16_bits_to_f32(hres[f][e].y >> 16)};
+                uint32_t vb[4];
+                float ss = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    vb[r] = f32_to_bf16_bits(hv[r] + yv[r]);
+                    const float v = bf16_bits_to_f32(vb[r]);
+                    ss = ss + v * v;
+                }
+                ss = ss + shfl_xor(ss, 16);
+                ss = ss + shfl_xor(ss, 32);
+                if (m < M) {
+                    const int n = n0 + (wn * NF + e) * 16;
+                    *reinterpret_cast<uint2*>(a.y + static_cast<size_t>(m) * N + n + 4 * g) =
+                            make_uint2(vb[0] | (vb[1] << 16), vb[2] | (vb[3] << 16));
+                    if (g == 0) a.ss_out[static_cast<size_t>(m) * nss + (n >> 4)] = ss;
+                }
+            }
+        }
+    } else {
+        // kEpiQkv: bf16 tile [BM][kTs] in LDS (the stages are free once every wave has left the loop)
+        __syncthreads();
+        uint16_t* tile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+        for (int f = 0; f < MF; ++f) {
+            const int r = (wm * MF + f) * 16 + i16;
+#pragma unroll
+            for (int e = 0; e < NF; ++e) {
+                uint2 v;
+                v.x = pack_bf16x2(acc[f][e][0], acc[f][e][1]);
+                v.y = pack_bf16x2(acc[f][e][2], acc[f][e][3]);
+                *reinterpret_cast<uint2*>(tile + r * kTs + (wn * NF + e) * 16 + 4 * g) = v;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < kIter; ++it) {
+            const int idx = it * 16 + grp;
+            qkv_task_load_x<128>(in[it], tile + min(idx / kHeads, BM - 1) * kTs + (idx % kHeads) * 128, gl);
+        }
+#pragma unroll
+        for (int it = 0; it < kIter; ++it) {
+            const int idx = it * 16 + grp;
+            const int m = m0 + idx / kHeads;
+            if (idx < kTasks && m < M) qkv_task_run<128, SM>(in[it], m, n0 / 128 + idx % kHeads, tslot[it], a.qkv, gl);
+        }
+    }
 }
 
 typedef void (*GemmFn)(uint16_t*, const uint16_t*, const uint16_t*, int, int, int);
@@ -691,4 +896,163 @@ extern "C" int cvh_gemm_bf16_nt_configs(int* codes, int capacity) {
 extern "C" int cvh_gemm_bf16_nt_config(int64_t M, int N, int K) {
     const cvh::GemmCfg* c = cvh::auto_cfg(M, N, K);
     return c ? c->code() : 0;
+}
+
+// ---- fused-epilogue entry points -------------------------------------------------------------
+namespace cvh {
+namespace {
+
+typedef void (*FusedFn)(const uint16_t*, const uint16_t*, int, int, int, FusedArgs);
+struct FusedCfg {
+    int code, bm, bn;
+    FusedFn fn;
+};
+constexpr int tiled_code(int mf, int nf, int wm, int wn, int st) {
+    return 100000 * (st ? st : 9) + 20000 + 1000 * mf + 100 * nf + 10 * wm + wn;
+}
+#define CVH_FUSED(MF, NF, WM, WN, S, EPI, RS, SM) \
+    FusedCfg{tiled_code(MF, NF, WM, WN, S), 16 * MF * WM, 16 * NF * WN, gemm_fused_kernel<MF, NF, WM, WN, S, EPI, RS, SM>}
+const FusedCfg kResidCfgs[] = {
+    CVH_FUSED(1, 1, 2, 2, 3, kEpiResid, false, 0), CVH_FUSED(1, 1, 2, 2, 0, kEpiResid, false, 0),
+    CVH_FUSED(1, 1, 4, 1, 3, kEpiResid, false, 0), CVH_FUSED(1, 1, 4, 1, 0, kEpiResid, false, 0),
+    CVH_FUSED(2, 1, 2, 2, 3, kEpiResid, false, 0), CVH_FUSED(1, 2, 2, 2, 3, kEpiResid, false, 0),
+    CVH_FUSED(2, 1, 4, 1, 3, kEpiResid, false, 0), CVH_FUSED(1, 1, 1, 4, 3, kEpiResid, false, 0),
+};
+const FusedCfg kSwigluRsCfgs[] = {
+    CVH_FUSED(1, 2, 4, 1, 3, kEpiSwiglu, true, 0), CVH_FUSED(1, 2, 2, 2, 3, kEpiSwiglu, true, 0),
+    CVH_FUSED(2, 2, 2, 2, 3, kEpiSwiglu, true, 0), CVH_FUSED(2, 4, 2, 2, 3, kEpiSwiglu, true, 0),
+    CVH_FUSED(1, 2, 1, 4, 3, kEpiSwiglu, true, 0),
+};
+#define CVH_QKV_CFGS(RS, SM)                                                                                 \
+    CVH_FUSED(1, 2, 1, 4, 3, kEpiQkv, RS, SM), CVH_FUSED(2, 2, 1, 4, 3, kEpiQkv, RS, SM),                    \
+    CVH_FUSED(1, 4, 2, 2, 3, kEpiQkv, RS, SM), CVH_FUSED(2, 4, 2, 2, 3, kEpiQkv, RS, SM)
+const FusedCfg kQkvCfgs[2][2][4] = {
+    {{CVH_QKV_CFGS(false, CVH_SCALE_PER_TOKEN_HEAD)}, {CVH_QKV_CFGS(false, CVH_SCALE_PER_TENSOR)}},
+    {{CVH_QKV_CFGS(true, CVH_SCALE_PER_TOKEN_HEAD)}, {CVH_QKV_CFGS(true, CVH_SCALE_PER_TENSOR)}},
+};
+#undef CVH_QKV_CFGS
+#undef CVH_FUSED
+
+enum { kFusedResidual = 0, kFusedSwigluRownorm = 1, kFusedQkv = 2 };
+
+template <size_t NC>
+const FusedCfg* find_fused(const FusedCfg (&t)[NC], int code) {
+    for (const FusedCfg& c : t)
+        if (c.code == code) return &c;
+    return nullptr;
+}
+
+// Automatic tile per row count (measured on MI355X for the Qwen3-0.6B decode shapes).
+int auto_fused_code(int kind, int64_t M) {
+    switch (kind) {
+        case kFusedResidual: return tiled_code(1, 1, 2, 2, 0);
+        case kFusedSwigluRownorm:
+            return M <= 64 ? tiled_code(1, 2, 4, 1, 3) : M <= 128 ? tiled_code(1, 2, 2, 2, 3) : tiled_code(2, 4, 2, 2, 3);
+        default: return M <= 128 ? tiled_code(1, 2, 1, 4, 3) : tiled_code(1, 4, 2, 2, 3);
+    }
+}
+
+const FusedCfg* fused_cfg(int kind, int code, bool rs, int sm) {
+    switch (kind) {
+        case kFusedResidual: return find_fused(kResidCfgs, code);
+        case kFusedSwigluRownorm: return find_fused(kSwigluRsCfgs, code);
+        case kFusedQkv: return find_fused(kQkvCfgs[rs ? 1 : 0][sm == CVH_SCALE_PER_TENSOR ? 1 : 0], code);
+        default: return nullptr;
+    }
+}
+
+int launch_fused(const FusedCfg* c, const void* x, const void* w, int64_t M, int N, int K, const FusedArgs& a,
+                 cvh_stream_t stream) {
+    if (!c || N % c->bn) return CVH_ERR_UNSUPPORTED;
+    const dim3 grid(N / c->bn, static_cast<unsigned>((M + c->bm - 1) / c->bm));
+    hipLaunchKernelGGL(c->fn, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<int>(M), N, K, a);
+    return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+}
+
+bool rs_shape_ok(int K) { return K % 256 == 0 && K / 256 <= kMaxRsQuads; }
+
+}  // namespace
+}  // namespace cvh
+
+extern "C" int cvh_gemm_bf16_nt_residual(void* resid, float* row_ss, const void* x, const void* w, int64_t M, int N,
+                                         int K, int config, cvh_stream_t stream) {
+    using namespace cvh;
+    if (M < 0 || N <= 0 || K <= 0) return CVH_ERR_INVALID_ARG;
+    if (M == 0) return CVH_OK;
+    if (!resid || !row_ss || !x || !w) return CVH_ERR_INVALID_ARG;
+    if (M > (1 << 20) || N % 16 || K % kChunk || N > (1 << 20)) return CVH_ERR_UNSUPPORTED;
+    FusedArgs a{};
+    a.y = static_cast<uint16_t*>(resid);
+    a.ss_out = row_ss;
+    const int code = config > 0 ? config : auto_fused_code(kFusedResidual, M);
+    return launch_fused(fused_cfg(kFusedResidual, code, false, 0), x, w, M, N, K, a, stream);
+}
+
+extern "C" int cvh_gemm_bf16_nt_swiglu_rownorm(void* act, const void* x, const float* row_ss, double eps,
+                                               const void* w, int64_t M, int I, int K, int config,
+                                               cvh_stream_t stream) {
+    using namespace cvh;
+    if (M < 0 || I <= 0 || K <= 0) return CVH_ERR_INVALID_ARG;
+    if (M == 0) return CVH_OK;
+    if (!act || !x || !row_ss || !w) return CVH_ERR_INVALID_ARG;
+    if (M > (1 << 20) || I % 16 || K % kChunk || I > (1 << 19) || !rs_shape_ok(K)) return CVH_ERR_UNSUPPORTED;
+    FusedArgs a{};
+    a.y = static_cast<uint16_t*>(act);
+    a.ss_in = row_ss;
+    a.eps_in = static_cast<float>(eps);
+    const int code = config > 0 ? config : auto_fused_code(kFusedSwigluRownorm, M);
+    return launch_fused(fused_cfg(kFusedSwigluRownorm, code, true, 0), x, w, M, 2 * I, K, a, stream);
+}
+
+extern "C" int cvh_gemm_qkv_norm_rope_kv_write_fp8(
+        void* q_out, const void* x, const float* row_ss, double x_eps, const void* w_qkv, const void* q_norm,
+        const void* k_norm, const float* cos_t, const float* sin_t, const int64_t* positions, const int64_t* slots,
+        uint8_t* k_cache, uint8_t* v_cache, float* k_scale, float* v_scale, int64_t num_tokens, int dim, int n_heads,
+        int n_kv_heads, int head_dim, int block_size, int scale_mode, double eps, int config, cvh_stream_t stream) {
+    using namespace cvh;
+    if (num_tokens < 0 || dim <= 0 || n_heads <= 0 || n_kv_heads <= 0) return CVH_ERR_INVALID_ARG;
+    if (num_tokens == 0) return CVH_OK;
+    if (!q_out || !x || !w_qkv || !q_norm || !k_norm || !cos_t || !sin_t || !positions || !slots || !k_cache ||
+        !v_cache || !k_scale || !v_scale)
+        return CVH_ERR_INVALID_ARG;
+    if (head_dim != 128 || num_tokens > (1 << 20) || dim % kChunk || (row_ss && !rs_shape_ok(dim)))
+        return CVH_ERR_UNSUPPORTED;
+    if (scale_mode != CVH_SCALE_PER_TOKEN_HEAD && scale_mode != CVH_SCALE_PER_TENSOR) return CVH_ERR_UNSUPPORTED;
+    int lg = 0;
+    while ((1 << lg) < block_size) ++lg;
+    if ((1 << lg) != block_size || lg < 4 || lg > 12) return CVH_ERR_UNSUPPORTED;
+    const int N = (n_heads + 2 * n_kv_heads) * head_dim;
+    FusedArgs a{};
+    a.ss_in = row_ss;
+    a.eps_in = static_cast<float>(x_eps);
+    a.positions = positions;
+    a.slots = slots;
+    a.qkv = QkvDst{static_cast<uint16_t*>(q_out), static_cast<const uint16_t*>(q_norm),
+                   static_cast<const uint16_t*>(k_norm), cos_t, sin_t, k_cache, v_cache, k_scale, v_scale, nullptr,
+                   nullptr, n_heads, n_kv_heads, lg, static_cast<float>(eps)};
+    const int code = config > 0 ? config : auto_fused_code(kFusedQkv, num_tokens);
+    return launch_fused(fused_cfg(kFusedQkv, code, row_ss != nullptr, scale_mode), x, w_qkv, num_tokens, N, dim, a,
+                        stream);
+}
+
+extern "C" int cvh_gemm_fused_configs(int kind, int* codes, int capacity) {
+    using namespace cvh;
+    const FusedCfg* t = nullptr;
+    int n = 0;
+    switch (kind) {
+        case kFusedResidual: t = kResidCfgs; n = static_cast<int>(sizeof(kResidCfgs) / sizeof(FusedCfg)); break;
+        case kFusedSwigluRownorm:
+            t = kSwigluRsCfgs;
+            n = static_cast<int>(sizeof(kSwigluRsCfgs) / sizeof(FusedCfg));
+            break;
+        case kFusedQkv: t = kQkvCfgs[0][0]; n = 4; break;
+        default: return 0;
+    }
+    for (int i = 0; i < n && codes && i < capacity; ++i) codes[i] = t[i].code;
+    return n;
+}
+
+extern "C" int cvh_gemm_fused_config(int kind, int64_t M) {
+    return kind >= 0 && kind <= 2 ? cvh::auto_fused_code(kind, M) : 0;
 }

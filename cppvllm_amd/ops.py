@@ -264,6 +264,80 @@ def linear(out, x, w, config: int = 0) -> None:
                                                       int(config), _stream(out)))
 
 
+FUSED_RESIDUAL, FUSED_SWIGLU_ROWNORM, FUSED_QKV = 0, 1, 2
+
+
+def row_ss_slots(n: int) -> int:
+    """Partial sums of squares per row that linear_residual writes for an N-wide row (N / 16)."""
+    return n // 16
+
+
+def linear_residual(resid, row_ss, x, w, config: int = 0) -> None:
+    """resid [M, N] <- bf16(resid + bf16(x . w^T)) (the residual add of add_rms_norm,
+    kernels/fused_ops.cu:70-73, in the projection's epilogue) and row_ss [M, N/16] <- the new
+    residual's sum of squares per 16 columns, which a *_rownorm projection turns into the row's
+    RMSNorm factor."""
+    M = x.size(0)
+    if M == 0:
+        return
+    _require_cuda(resid, row_ss, x, w)
+    N, K = w.shape
+    if tuple(resid.shape) != (M, N) or x.size(1) != K or tuple(row_ss.shape) != (M, row_ss_slots(N)):
+        raise ValueError(f"linear_residual: shapes resid {tuple(resid.shape)}, x {tuple(x.shape)}, w {tuple(w.shape)}, "
+                         f"row_ss {tuple(row_ss.shape)}")
+    if not (x.dtype == w.dtype == resid.dtype == torch.bfloat16 and row_ss.dtype == torch.float32):
+        raise ValueError("linear_residual: bf16 tensors and a float32 row_ss")
+    check("gemm_bf16_nt_residual", _lib.lib().cvh_gemm_bf16_nt_residual(
+        resid.data_ptr(), row_ss.data_ptr(), x.data_ptr(), w.data_ptr(), M, N, K, int(config), _stream(x)))
+
+
+def fold_norm_gain(w, gain) -> torch.Tensor:
+    """w' = bf16(w * gain) over the input columns: the weight a *_rownorm projection takes for an
+    RMSNorm with that gain."""
+    return (w.float() * gain.float()[None, :]).to(torch.bfloat16)
+
+
+def linear_swiglu_rownorm(act, x, row_ss, eps: float, w_folded, config: int = 0) -> None:
+    """act [M, I] = swiglu(rms(x) . w^T) with x the raw residual rows, rms's factor from row_ss
+    (linear_residual) and its gain folded into w (fold_norm_gain of the 16-row interleaved gate/up
+    weight)."""
+    M = x.size(0)
+    if M == 0:
+        return
+    _require_cuda(act, x, row_ss, w_folded)
+    N, K = w_folded.shape
+    if x.size(1) != K or tuple(act.shape) != (M, N // 2) or tuple(row_ss.shape) != (M, row_ss_slots(K)):
+        raise ValueError("linear_swiglu_rownorm: shapes")
+    check("gemm_bf16_nt_swiglu_rownorm", _lib.lib().cvh_gemm_bf16_nt_swiglu_rownorm(
+        act.data_ptr(), x.data_ptr(), row_ss.data_ptr(), float(eps), w_folded.data_ptr(), M, N // 2, K, int(config),
+        _stream(x)))
+
+
+def qkv_norm_rope_kv_write_fp8(q_out, x, row_ss, x_eps: float, w_qkv, q_norm, k_norm, cos, sin, positions, slots,
+                               k_cache, v_cache, k_scale, v_scale, n_heads: int, n_kv_heads: int, eps: float,
+                               config: int = 0) -> None:
+    """The QKV projection with qk_norm_rope_kv_write_fp8 in its epilogue: q_out [T, H, HD] and the
+    K/V cache writes of fused.qk_norm_rope_kv_write_fp8 over qkv = x . w_qkv^T, without the qkv
+    tensor. row_ss None: x is the normed input as is; else x is the raw residual, normed by the
+    factor row_ss gives, with the norm gain folded into w_qkv (fold_norm_gain)."""
+    T = x.size(0)
+    if T == 0:
+        return
+    _require_cuda(q_out, x, row_ss, w_qkv, q_norm, k_norm, cos, sin, positions, slots, k_cache, v_cache, k_scale,
+                  v_scale)
+    N, D = w_qkv.shape
+    HD = q_out.size(2)
+    if x.size(1) != D or N != (n_heads + 2 * n_kv_heads) * HD or tuple(q_out.shape[:2]) != (T, n_heads):
+        raise ValueError("qkv_norm_rope_kv_write_fp8: shapes")
+    if row_ss is not None and tuple(row_ss.shape) != (T, row_ss_slots(D)):
+        raise ValueError("qkv_norm_rope_kv_write_fp8: row_ss shape")
+    check("gemm_qkv_norm_rope_kv_write_fp8", _lib.lib().cvh_gemm_qkv_norm_rope_kv_write_fp8(
+        q_out.data_ptr(), x.data_ptr(), _ptr(row_ss), float(x_eps), w_qkv.data_ptr(), q_norm.data_ptr(),
+        k_norm.data_ptr(), cos.data_ptr(), sin.data_ptr(), positions.data_ptr(), slots.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(), T, D, int(n_heads), int(n_kv_heads), HD,
+        k_cache.size(1), _scale_mode(k_scale), float(eps), int(config), _stream(x)))
+
+
 def interleave_gate_up(w_gate_up: torch.Tensor) -> torch.Tensor:
     """[2I, K] gate-then-up weight rows -> the 16-row interleaved layout linear_swiglu takes."""
     n, k = w_gate_up.shape

@@ -35,6 +35,11 @@ fused = ops.fused
 # Qwen3-0.6B projection shapes and the tied lm_head).
 GEMM_MAX_ROWS = 256
 LM_HEAD_MAX_ROWS = 64
+# Row counts from which the projections with fused layer-boundary epilogues (residual add + norm
+# partials, row-normed inputs, QK-norm/RoPE/KV write) beat the projection + standalone-kernel
+# sequence (measured per decode layer on MI355X: 16 rows 35.2 -> 34.8 us, 96 rows 43.8 -> 36.9,
+# 256 rows 50.1 -> 44.3; at 1 row 31.4 -> 33.8).
+FUSED_MIN_ROWS = 16
 
 
 def _linear(x, w, max_rows: int = GEMM_MAX_ROWS):
@@ -115,6 +120,18 @@ class Qwen3:
         cos, sin = ops.rope_tables(c.max_seq_len, HD, c.rope_theta)
         self.cos, self.sin = cos.to(device), sin.to(device)
         self.scale = 1.0 / math.sqrt(HD)
+        self.unit_gain = ones(D)
+        self.fold_gains()
+
+    def fold_gains(self) -> None:
+        """Weights of the fused decode path: the input norms' gains multiplied into the columns of
+        the projections they feed (ops.fold_norm_gain; the same tensor where the gain is all ones).
+        Call again after changing attn_norm / ffn_norm."""
+        c = self.cfg
+        self.fused_ok = (c.head_dim == 128 and c.dim % 256 == 0 and c.dim <= 1024 and self.gate_up_interleaved)
+        fold = lambda w, gain: w if bool((gain == 1).all()) else ops.fold_norm_gain(w, gain)  # noqa: E731
+        self.wqkv_f = [fold(w, g) for w, g in zip(self.wqkv, self.attn_norm)]
+        self.w_gu_f = [fold(w, g) for w, g in zip(self.w_gu, self.ffn_norm)] if self.fused_ok else []
 
     def forward(self, cache: KVCache, tokens, positions, cu_seqlens, block_tables, workspace, planned: bool,
                 shared_blocks=None):
@@ -129,7 +146,6 @@ class Qwen3:
         h = torch.empty((T, D), dtype=bf16, device=dev)
         ops.embedding(h, self.embed, tokens)
         x = torch.empty_like(h)
-        fused.rms_norm(x, h, self.attn_norm[0], eps)
         shared = planned and shared_blocks is not None
         if planned:   # shared_blocks: per-row leading blocks shared with other rows, read cache-resident
             ops.paged_attention_plan(block_tables, seq, kvl, H, KV, HD, cache.block_size, workspace,
@@ -141,16 +157,41 @@ class Qwen3:
         # multi-query kernel; decode rows take the stream-K decode kernel
         S = cu_seqlens.numel() - 1
         multi_query = not planned and T >= 2 * S and ops.prefill_supported(H, KV, HD)
-        for li in range(c.n_layers):
-            kc, vc, ks, vs = cache.layers[li]
-            qkv = _linear(x, self.wqkv[li])
-            fused.qk_norm_rope_kv_write_fp8(q, qkv, self.q_norm[li], self.k_norm[li], self.cos, self.sin, positions,
-                                            slot, kc, vc, ks, vs, None, None, H, KV, eps)
+
+        def attention(li, kc, vc, ks, vs):
             if multi_query:
                 ops.paged_attention_fp8_prefill(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale)
             else:
                 ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
                                         workspace=workspace, planned=planned, shared=shared)
+
+        if self.fused_ok and FUSED_MIN_ROWS <= T <= GEMM_MAX_ROWS:
+            # Layer boundaries in the projections' epilogues: o_proj / down_proj add into the
+            # residual h and leave its per-16-column sums of squares in ss; qkv / gate-up take h
+            # raw and apply the row's RMS factor from ss (gains folded into their weights); qkv
+            # runs the QK-norm / RoPE / FP8 K/V write on its own output tile. Layer 0's input is
+            # normed with a unit gain.
+            ss = torch.empty((T, ops.row_ss_slots(D)), dtype=torch.float32, device=dev)
+            fused.rms_norm(x, h, self.unit_gain, eps)
+            for li in range(c.n_layers):
+                kc, vc, ks, vs = cache.layers[li]
+                ops.qkv_norm_rope_kv_write_fp8(q, x if li == 0 else h, None if li == 0 else ss, eps, self.wqkv_f[li],
+                                               self.q_norm[li], self.k_norm[li], self.cos, self.sin, positions, slot,
+                                               kc, vc, ks, vs, H, KV, eps)
+                attention(li, kc, vc, ks, vs)
+                ops.linear_residual(h, ss, att.view(T, H * HD), self.wo[li])
+                ops.linear_swiglu_rownorm(act, h, ss, eps, self.w_gu_f[li])
+                ops.linear_residual(h, ss, act, self.w_down[li])
+            fused.rms_norm(x, h, self.final_norm, eps)
+            return x
+
+        fused.rms_norm(x, h, self.attn_norm[0], eps)
+        for li in range(c.n_layers):
+            kc, vc, ks, vs = cache.layers[li]
+            qkv = _linear(x, self.wqkv[li])
+            fused.qk_norm_rope_kv_write_fp8(q, qkv, self.q_norm[li], self.k_norm[li], self.cos, self.sin, positions,
+                                            slot, kc, vc, ks, vs, None, None, H, KV, eps)
+            attention(li, kc, vc, ks, vs)
             o = _linear(att.view(T, H * HD), self.wo[li])
             fused.add_rms_norm(h, o, self.ffn_norm[li], x, eps)
             if self.gate_up_interleaved and T <= GEMM_MAX_ROWS and ops.gemm_supported(2 * I, D):

@@ -336,6 +336,47 @@ int cvh_gemm_bf16_nt_swiglu_config(int64_t M, int I, int K);
 /* Codes of the compiled SwiGLU-epilogue configurations (as cvh_gemm_bf16_nt_configs). */
 int cvh_gemm_bf16_nt_swiglu_configs(int* codes, int capacity);
 
+/* ---- Projections with the layer boundary fused into their epilogues (decode steps) ----------
+ * The reference runs the projection, then a separate norm or QK-norm launch
+ * (model/model_architecture.cpp:155-188, kernels/fused_ops.cu:61-207). These entry points do both
+ * in one kernel; all take tiled configuration codes (as cvh_gemm_bf16_nt) listed by
+ * cvh_gemm_fused_configs(kind), kind 0 = residual, 1 = SwiGLU-rownorm, 2 = QKV; config 0 picks the
+ * measured best for the row count (cvh_gemm_fused_config).
+ *
+ * Residual epilogue (o_proj, down_proj): resid[M][N] <- bf16(resid + bf16(x . w^T)), the residual
+ * add of cvh_add_rms_norm bit for bit, and row_ss[M][N/16] <- for each 16 columns n..n+15 of the new
+ * residual v, the sum of v^2 as lanes holding columns 4j..4j+3 sum their four in order and the four
+ * lane sums combine as (s0 + s1) + (s2 + s3). The row's norm sum is the in-order sum of its N/16
+ * partials. Requires N % 32 == 0 (the tile width), K % 128 == 0. */
+int cvh_gemm_bf16_nt_residual(void* resid, float* row_ss, const void* x, const void* w, int64_t M, int N, int K,
+                              int config, cvh_stream_t stream);
+/* Row-normed gate/up with the SwiGLU epilogue: x is the raw residual (the rows
+ * cvh_gemm_bf16_nt_residual wrote), inv[m] = 1 / sqrt(sum(row_ss[m][0..K/16)) / K + eps) with the
+ * sum taken as each of 4 lanes summing K/64 consecutive partials in order, then (q0 + q1) + (q2 + q3);
+ * the accumulator is multiplied by inv before cvh_gemm_bf16_nt_swiglu's epilogue. w is the
+ * interleaved gate/up weight with the RMSNorm gain multiplied into its columns and rounded to bf16,
+ * so the result stands for swiglu(bf16(bf16(x * inv) * gain) . w^T) up to those roundings.
+ * Requires K % 256 == 0 and K <= 1024. */
+int cvh_gemm_bf16_nt_swiglu_rownorm(void* act, const void* x, const float* row_ss, double eps, const void* w,
+                                    int64_t M, int I, int K, int config, cvh_stream_t stream);
+/* QKV projection with cvh_qk_norm_rope_kv_write_fp8 in its epilogue: the bf16 tile of
+ * qkv = x . w_qkv^T ([T][(H + 2KV) * 128]) is kept on chip and each (token, head) of it runs the
+ * standalone kernel's task, so q_out and the cache bytes equal cvh_gemm_bf16_nt (same tiled config)
+ * followed by cvh_qk_norm_rope_kv_write_fp8, bit for bit, when row_ss is NULL. With row_ss, x is the
+ * raw residual and the accumulator is first multiplied by the row's RMSNorm factor (as
+ * cvh_gemm_bf16_nt_swiglu_rownorm; x_eps is that norm's eps, w_qkv carries its gain). No dense K/V
+ * copies. Requires head_dim == 128, dim % 128 == 0 (with row_ss: dim % 256 == 0, dim <= 1024). */
+int cvh_gemm_qkv_norm_rope_kv_write_fp8(void* q_out, const void* x, const float* row_ss, double x_eps,
+                                        const void* w_qkv, const void* q_norm, const void* k_norm, const float* cos_t,
+                                        const float* sin_t, const int64_t* positions, const int64_t* slots,
+                                        uint8_t* k_cache, uint8_t* v_cache, float* k_scale, float* v_scale,
+                                        int64_t num_tokens, int dim, int n_heads, int n_kv_heads, int head_dim,
+                                        int block_size, int scale_mode, double eps, int config, cvh_stream_t stream);
+/* Codes of the compiled configurations of a fused kind (as cvh_gemm_bf16_nt_configs); returns the count. */
+int cvh_gemm_fused_configs(int kind, int* codes, int capacity);
+/* The configuration a fused kind picks for M rows with config == 0. */
+int cvh_gemm_fused_config(int kind, int64_t M);
+
 /* Library version string (static storage). */
 const char* cvh_version(void);
 

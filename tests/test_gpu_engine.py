@@ -147,6 +147,60 @@ def test_prefill_and_decode_match_torch_reference():
         assert err.max().item() < 0.25 and err.mean().item() < 1.5e-2
 
 
+def test_fused_path_with_norm_gains_matches_torch_reference():
+    """Batches of 16..256 rows take the projections with fused epilogues (residual + norm partials,
+    row-normed inputs with the gains folded into the weights, QK-norm/RoPE/KV write in the QKV
+    epilogue). With random norm gains its rounding points differ from the reference's (the normed
+    input is not rounded, the gain-scaled weight is): prefill and decode rows must stay within
+    FUSED_X times the error the unfused path (the reference's rounding points, same kernels
+    otherwise) shows against the torch fp32 restatement (measured: 1.6-1.8x), and within max-abs
+    0.4 / mean-abs 0.04 (random gains widen both paths' errors)."""
+    FUSED_X = 2.5
+    say("runner: fused-epilogue path with random norm gains vs torch fp32 reference (2 layers)")
+    eng = _engine(blocks=128)
+    r, m = eng.runner, eng.model
+    g = torch.Generator().manual_seed(33)
+    gain = lambda n: (torch.rand((n,), generator=g) + 0.5).to(torch.bfloat16).to(DEV)  # noqa: E731
+    c = m.cfg
+    m.attn_norm = [gain(c.dim) for _ in range(c.n_layers)]
+    m.ffn_norm = [gain(c.dim) for _ in range(c.n_layers)]
+    m.q_norm = [gain(c.head_dim) for _ in range(c.n_layers)]
+    m.k_norm = [gain(c.head_dim) for _ in range(c.n_layers)]
+    m.final_norm = gain(c.dim)
+    m.fold_gains()
+    lens = torch.randint(3, 16, (20,), generator=g).tolist()   # len + 1 <= 16: one block each, both batches
+    b = _batch(lens, [0] * 20, 16)
+    b.tokens[:] = torch.randint(0, SMALL.vocab_size, (b.num_tokens,), generator=g).numpy()
+    new = torch.randint(0, SMALL.vocab_size, (20,), generator=g).numpy()
+    dec = _batch([1] * 20, lens, 16)
+    dec.tokens[:] = new
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)  # noqa: E731
+
+    def run(bt):
+        return m.forward(eng.cache, d(bt.tokens), d(bt.positions), d(bt.cu_seqlens), d(bt.block_tables), r.ws_eager,
+                         planned=False).float()
+
+    want_p = torch.cat([ref_forward(m, d(b.tokens[b.cu_seqlens[j]:b.cu_seqlens[j + 1]]),
+                                    d(b.positions[b.cu_seqlens[j]:b.cu_seqlens[j + 1]])) for j in range(20)])
+    want_d = torch.stack([ref_forward(m, d(np.concatenate([b.tokens[b.cu_seqlens[j]:b.cu_seqlens[j + 1]],
+                                                           new[j:j + 1]])),
+                                      torch.arange(lens[j] + 1, device=DEV))[-1] for j in range(20)])
+    errs = {}
+    for fused_path in (False, True):
+        m.fused_ok = fused_path
+        say(f"  {'fused' if fused_path else 'unfused'}: prefill of 20 sequences ({b.num_tokens} rows), "
+            "then a 20-row decode step")
+        ep = (run(b) - want_p).abs()
+        ed = (run(dec) - want_d).abs()
+        errs[fused_path] = [(e.max().item(), e.mean().item()) for e in (ep, ed)]
+        say(f"    prefill max {errs[fused_path][0][0]:.3e} mean {errs[fused_path][0][1]:.3e}; "
+            f"decode max {errs[fused_path][1][0]:.3e} mean {errs[fused_path][1][1]:.3e}")
+    m.fold_gains()
+    for (fm, fa), (um, ua) in zip(errs[True], errs[False]):
+        assert fm < 0.4 and fa < 0.04
+        assert fm <= FUSED_X * um and fa <= FUSED_X * ua
+
+
 def test_graph_decode_equals_eager_decode():
     say("runner: graph replay vs eager forward for the same decode rows")
     eng = _engine()
