@@ -275,6 +275,17 @@ class ModelRunner:
         self.shared_replays = 0
         if not enforce_eager:
             self.capture_graphs()
+        self.warm_sampler()
+
+    def warm_sampler(self) -> None:
+        """Run the lm_head + sampler once per row count above LM_HEAD_MAX_ROWS (up to the
+        sequence cap) at start-up: hipBLASLt picks its algorithm on the first call of each shape,
+        which inside a run costs ~0.15 s over config 5's decode batch sizes."""
+        c = self.model.cfg
+        dev = self.model.device
+        for S in range(LM_HEAD_MAX_ROWS + 1, self.max_seqs + 1):
+            self.model.sample(torch.zeros((S, c.dim), dtype=torch.bfloat16, device=dev), self.d_tmp[:S])
+        torch.cuda.synchronize()
 
     # ---- decode graphs -------------------------------------------------------------------------
     def _stage_graph_rows(self, toks, pos, tables, B: int, feed=None, slot: int = 0, shared=None) -> bool:
