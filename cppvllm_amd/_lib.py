@@ -40,6 +40,10 @@ SIGNATURES = {
                                                   i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
                                               f64, vp]),
+    "cvh_paged_attention_prefill_workspace_bytes": (sz, [i64]),
+    "cvh_paged_attention_prefill_plan": (i32, [vp, vp, i64, i64, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_prefill_planned": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32,
+                                                      i32, f64, vp, sz, vp]),
     "cvh_paged_attention_plan": (i32, [vp, i64, vp, vp, i64, i32, i32, i32, i32, i32, vp, sz, vp]),
     "cvh_paged_attention_plan_shared": (i32, [vp, i64, vp, vp, vp, i64, i32, i32, i32, i32, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned_shared": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32,

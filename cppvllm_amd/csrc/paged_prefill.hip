@@ -98,23 +98,32 @@ struct TileRegs {
     float ks, vs;
 };
 
-template <int REP, int SCALE_MODE>
-__global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
+// KSPLIT: 8 waves; waves 4..7 take the second half of every run's key tiles for the same 64
+// tokens, with their own LDS tiles, and hand their (m, l, O) to waves 0..3 through LDS at the end.
+template <int REP, int SCALE_MODE, bool KSPLIT>
+__global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_prefill_kernel(
         uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
         const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
         const int64_t* __restrict__ tables, int64_t W, const int64_t* __restrict__ token_seq,
-        const int64_t* __restrict__ token_kv_len, int T, int H, int KV, int lg_bs, float scale_log2) {
-    __shared__ __align__(16) PrefillLds sm;
-    const int tid = threadIdx.x, lane = tid & 63;
+        const int64_t* __restrict__ token_kv_len, int T, int H, int KV, int lg_bs, float scale_log2,
+        const int* __restrict__ order) {
+    constexpr int NH = KSPLIT ? 2 : 1;
+    __shared__ __align__(16) PrefillLds smv[NH];
+    const int tid = threadIdx.x & 255, lane = tid & 63;
+    const int half = KSPLIT ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 8) : 0;
+    PrefillLds& sm = smv[half];
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kvh = blockIdx.y;
-    const int t0 = blockIdx.x * kWgTok;
+    // item = (64-token group, kv head): blockIdx.x walks the groups of kv head blockIdx.y, or with
+    // a plan, 1-D blockIdx.x walks order[] (groups by descending key-tile count) x kv heads
+    const int item_group = order ? order[blockIdx.x / KV] : static_cast<int>(blockIdx.x);
+    const int kvh = order ? static_cast<int>(blockIdx.x % KV) : static_cast<int>(blockIdx.y);
+    const int t0 = item_group * kWgTok;
     const int g = lane >> 4, i16 = lane & 15;
     const int BS = 1 << lg_bs, bs_mask = BS - 1;
     const int64_t row_bytes = static_cast<int64_t>(KV) * kHD;      // one slot row, all kv heads
 
     // token metadata of the 64 tokens -> LDS (clamped like the decode kernel)
-    if (tid < kWgTok) {
+    if (half == 0 && tid < kWgTok) {
         const int t = t0 + tid;
         int64_t sq = -1, kv = 0;
         if (t < T) {
@@ -123,8 +132,8 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
             if (sq < 0 || kv < 0) kv = 0;
             if (kv > (W << lg_bs)) kv = W << lg_bs;
         }
-        sm.tseq[tid] = sq;
-        sm.tkvl[tid] = static_cast<int>(kv);
+        smv[0].tseq[tid] = sq;
+        smv[0].tkvl[tid] = static_cast<int>(kv);
     }
     // this wave's 16 query rows (token t0 + 16w + i16, heads kvh*REP + rb) as MFMA B operands:
     // step s = 2c + h covers d = c*64 + g*16 + h*8 + 0..7
@@ -155,10 +164,10 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
     const float vs_tensor = SCALE_MODE == CVH_SCALE_PER_TENSOR ? vsc[0] : 0.f;
 
     // every wave sees all 64 tokens (lane l <-> token l) so the run loop is uniform across waves
-    const int64_t all_seq = sm.tseq[lane];
-    const int all_kvl = sm.tkvl[lane];
-    const int64_t my_seq = sm.tseq[16 * w + i16];
-    const int my_kvl = sm.tkvl[16 * w + i16];
+    const int64_t all_seq = smv[0].tseq[lane];
+    const int all_kvl = smv[0].tkvl[lane];
+    const int64_t my_seq = smv[0].tseq[16 * w + i16];
+    const int my_kvl = smv[0].tkvl[16 * w + i16];
     uint64_t todo = __builtin_amdgcn_ballot_w64(all_kvl > 0);
     while (todo) {
         const int leader = __builtin_ctzll(todo);
@@ -171,6 +180,11 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) kmax_l = max(kmax_l, __shfl_xor(kmax_l, d, 64));
         const int kmax = __builtin_amdgcn_readfirstlane(kmax_l);
+        // this half's key range: tiles [0, n0) or [n0, ntiles); both halves run n0 iterations
+        const int ntiles = (kmax + kTile - 1) / kTile;
+        const int n0 = KSPLIT ? (ntiles + 1) >> 1 : ntiles;
+        const int kbeg = half ? n0 * kTile : 0;
+        const int kend = half ? kmax : min(kmax, n0 * kTile);
         const int64_t* trow = tables + rseq * W;
         const int row_kvl = (my_seq == rseq) ? my_kvl : 0;
         // keys this wave's rows need in the run: tiles past it are staged for the other waves only
@@ -182,12 +196,12 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
         // cooperative load of tile kb0 into registers (keys >= kmax and negative table entries
         // read as zeros; a negative entry inside a context is invalid input)
         auto load_tile = [&](int kb0, TileRegs& r) {
-            const bool any = kb0 < kmax;
+            const bool any = kb0 < kend;
             const int64_t blk0 = any ? trow[kb0 >> lg_bs] : -1;
-            const int64_t blk1 = BS < kTile ? (kb0 + 16 < kmax ? trow[(kb0 + 16) >> lg_bs] : -1) : blk0;
+            const int64_t blk1 = BS < kTile ? (kb0 + 16 < kend ? trow[(kb0 + 16) >> lg_bs] : -1) : blk0;
             auto slot_of = [&](int key, bool& ok) -> int64_t {
                 const int64_t b = (BS < kTile && key >= 16) ? blk1 : blk0;
-                ok = b >= 0 && kb0 + key < kmax;
+                ok = b >= 0 && kb0 + key < kend;
                 return (b << lg_bs) + ((kb0 + key) & bs_mask);
             };
             bool ok;
@@ -327,19 +341,60 @@ __global__ __launch_bounds__(256, 2) void paged_prefill_kernel(
         // two-stage pipeline: tile i is multiplied from LDS while tile i+1 sits in registers
         // (stored to the other buffer after the multiply) and tile i+2's loads are in flight
         TileRegs rg;
-        load_tile(0, rg);
+        load_tile(kbeg, rg);
         store_tile(0, rg);
-        load_tile(kTile, rg);
+        load_tile(kbeg + kTile, rg);
         __syncthreads();
-        for (int i = 0, kb0 = 0; kb0 < kmax; ++i, kb0 += kTile) {
+        for (int i = 0, kb0 = kbeg; i < n0; ++i, kb0 += kTile) {
             const int buf = i & 1;
-            if (kb0 < wave_kmax) compute(buf, kb0);
-            if (kb0 + kTile < kmax) {
+            if (kb0 < kend && kb0 < wave_kmax) compute(buf, kb0);
+            if (kb0 + kTile < kend) {
                 store_tile(buf ^ 1, rg);
                 load_tile(kb0 + 2 * kTile, rg);
             }
             __syncthreads();
         }
+    }
+
+    if constexpr (KSPLIT) {
+        // waves 4..7 -> LDS (the tiles are no longer read): per (rb, value) a row of 256 lanes
+        constexpr int kVals = 2 + 32;
+        static_assert(sizeof(smv) >= REP * kVals * 256 * sizeof(float), "combine buffer");
+        float* xs = reinterpret_cast<float*>(smv);
+        if (half) {
+#pragma unroll
+            for (int rb = 0; rb < REP; ++rb) {
+                float* d = xs + rb * kVals * 256 + tid;
+                d[0] = m[rb];
+                d[256] = sum_groups(lsum[rb]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d[(2 + 4 * j + e) * 256] = o[rb][j][e];
+            }
+        }
+        __syncthreads();
+        if (half) return;
+        if (tq >= T) return;
+#pragma unroll
+        for (int rb = 0; rb < REP; ++rb) {
+            const float* d = xs + rb * kVals * 256 + tid;
+            const float m1 = d[0], l1 = d[256];
+            const float mn = fmaxf(m[rb], m1);
+            const float a0 = __builtin_amdgcn_exp2f(m[rb] - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
+            const float l = sum_groups(lsum[rb]) * a0 + l1 * a1;
+            const float inv = l > 0.f ? 1.0f / l : 0.f;
+            uint16_t* orow = out + (static_cast<int64_t>(tq) * H + kvh * REP + rb) * kHD;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = (o[rb][j][e] * a0 + d[(2 + 4 * j + e) * 256] * a1) * inv;
+                *reinterpret_cast<uint2*>(orow + j * 16 + g * 4) =
+                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            }
+        }
+        return;
     }
 
     if (tq >= T) return;
@@ -367,23 +422,82 @@ int ilog2_exact(int v) {
 template <int REP, int SM>
 int launch_rep(uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_t* vc, const float* ks,
                const float* vs, const int64_t* tables, int64_t W, const int64_t* tseq, const int64_t* tkvl, int T,
-               int H, int KV, int lg, float sl2, hipStream_t s) {
+               int H, int KV, int lg, float sl2, const int* order, hipStream_t s) {
     const unsigned gx = static_cast<unsigned>((T + kWgTok - 1) / kWgTok);
-    paged_prefill_kernel<REP, SM><<<dim3(gx, KV), 256, 0, s>>>(out, q, kc, vc, ks, vs, tables, W, tseq, tkvl, T, H, KV,
-                                                               lg, sl2);
+    if (order) {
+        // longest items first, each split over two 4-wave halves: the dispatcher starts the long
+        // items at once and the short ones fill the slots they leave
+        paged_prefill_kernel<REP, SM, true><<<dim3(gx * KV), 512, 0, s>>>(out, q, kc, vc, ks, vs, tables, W, tseq,
+                                                                           tkvl, T, H, KV, lg, sl2, order);
+    } else {
+        paged_prefill_kernel<REP, SM, false><<<dim3(gx, KV), 256, 0, s>>>(out, q, kc, vc, ks, vs, tables, W, tseq,
+                                                                           tkvl, T, H, KV, lg, sl2, nullptr);
+    }
     return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+}
+
+// ---- plan: 64-token groups by descending key-tile count -------------------------------------
+// One 1024-thread workgroup: the cost of a group is its largest clamped token_kv_len in 32-key
+// tiles (buckets capped at kCostBuckets - 1); a counting sort writes the groups in descending
+// cost order (ties in any order: the order only steers the dispatcher, results do not depend on
+// it). Workspace: cost[groups] then order[groups] (int32).
+constexpr int kCostBuckets = 1024;
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const int64_t* __restrict__ token_seq,
+                                                                    const int64_t* __restrict__ token_kv_len, int T,
+                                                                    int64_t max_keys, int* __restrict__ cost,
+                                                                    int* __restrict__ order) {
+    __shared__ int hist[kCostBuckets];
+    __shared__ int scan[kCostBuckets];
+    const int tid = threadIdx.x;
+    const int groups = (T + kWgTok - 1) / kWgTok;
+    for (int i = tid; i < kCostBuckets; i += kPlanThreads) hist[i] = 0;
+    __syncthreads();
+    for (int gi = tid; gi < groups; gi += kPlanThreads) {
+        int64_t kmax = 0;
+        for (int j = 0; j < kWgTok; ++j) {
+            const int t = gi * kWgTok + j;
+            if (t >= T) break;
+            const int64_t kv = token_kv_len[t];
+            if (token_seq[t] >= 0 && kv > kmax) kmax = kv;
+        }
+        kmax = min(kmax, max_keys);
+        const int c = static_cast<int>(min<int64_t>((kmax + kTile - 1) / kTile, kCostBuckets - 1));
+        cost[gi] = c;
+        atomicAdd(&hist[c], 1);
+    }
+    __syncthreads();
+    // exclusive scan in descending cost: start[c] = number of groups with cost > c
+    const int rb = kCostBuckets - 1 - tid;           // bucket of this thread, reversed
+    int v = tid < kCostBuckets ? hist[rb] : 0;
+    scan[tid] = v;
+    __syncthreads();
+    for (int d = 1; d < kCostBuckets; d <<= 1) {
+        const int add = tid >= d ? scan[tid - d] : 0;
+        __syncthreads();
+        scan[tid] += add;
+        __syncthreads();
+    }
+    if (tid < kCostBuckets) hist[rb] = scan[tid] - v;   // exclusive
+    __syncthreads();
+    for (int gi = tid; gi < groups; gi += kPlanThreads) order[atomicAdd(&hist[cost[gi]], 1)] = gi;
+}
+
+size_t plan_bytes(int64_t num_tokens) {
+    const int64_t groups = (num_tokens + kWgTok - 1) / kWgTok;
+    return static_cast<size_t>(2 * groups) * sizeof(int);
 }
 
 }  // namespace
 }  // namespace cvh
 
-extern "C" int cvh_paged_attention_fp8_prefill(void* out, const void* q, const uint8_t* k_cache,
-                                               const uint8_t* v_cache, const float* k_scale, const float* v_scale,
-                                               const int64_t* block_tables, int64_t table_width,
-                                               const int64_t* token_seq, const int64_t* token_kv_len,
-                                               int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
-                                               int block_size, int scale_mode, double scale, cvh_stream_t stream) {
-    using namespace cvh;
+namespace cvh {
+namespace {
+int prefill_entry(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache, const float* k_scale,
+                  const float* v_scale, const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
+                  const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                  int block_size, int scale_mode, double scale, const int* order, cvh_stream_t stream) {
     if (num_tokens < 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width < 0) return CVH_ERR_INVALID_ARG;
     if (num_tokens == 0) return CVH_OK;
     if (table_width == 0) return CVH_ERR_INVALID_ARG;
@@ -396,24 +510,70 @@ extern "C" int cvh_paged_attention_fp8_prefill(void* out, const void* q, const u
     if (scale_mode != CVH_SCALE_PER_TOKEN_HEAD && scale_mode != CVH_SCALE_PER_TENSOR) return CVH_ERR_UNSUPPORTED;
     if (num_tokens > (int64_t{1} << 30)) return CVH_ERR_UNSUPPORTED;
     if (table_width > (int64_t{0x7fffffff} >> lg)) return CVH_ERR_UNSUPPORTED;    // contexts < 2^31 keys
+    if (order && (num_tokens + kWgTok - 1) / kWgTok * n_kv_heads > 0x7fffffff) return CVH_ERR_UNSUPPORTED;
     auto s = reinterpret_cast<hipStream_t>(stream);
     const float sl2 = static_cast<float>(scale) * kLog2eP;
     auto* o = static_cast<uint16_t*>(out);
     auto* qq = static_cast<const uint16_t*>(q);
     const int T = static_cast<int>(num_tokens);
-    if (rep == 1) {
-        if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-            return launch_rep<1, CVH_SCALE_PER_TOKEN_HEAD>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables,
-                                                           table_width, token_seq, token_kv_len, T, n_heads,
-                                                           n_kv_heads, lg, sl2, s);
-        return launch_rep<1, CVH_SCALE_PER_TENSOR>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables,
-                                                   table_width, token_seq, token_kv_len, T, n_heads, n_kv_heads, lg,
-                                                   sl2, s);
-    }
-    if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
-        return launch_rep<2, CVH_SCALE_PER_TOKEN_HEAD>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables,
-                                                       table_width, token_seq, token_kv_len, T, n_heads, n_kv_heads,
-                                                       lg, sl2, s);
-    return launch_rep<2, CVH_SCALE_PER_TENSOR>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables, table_width,
-                                               token_seq, token_kv_len, T, n_heads, n_kv_heads, lg, sl2, s);
+#define CVH_PF(R, SM)                                                                                             \
+    launch_rep<R, SM>(o, qq, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq, token_kv_len, \
+                      T, n_heads, n_kv_heads, lg, sl2, order, s)
+    if (rep == 1)
+        return scale_mode == CVH_SCALE_PER_TOKEN_HEAD ? CVH_PF(1, CVH_SCALE_PER_TOKEN_HEAD)
+                                                      : CVH_PF(1, CVH_SCALE_PER_TENSOR);
+    return scale_mode == CVH_SCALE_PER_TOKEN_HEAD ? CVH_PF(2, CVH_SCALE_PER_TOKEN_HEAD) : CVH_PF(2, CVH_SCALE_PER_TENSOR);
+#undef CVH_PF
+}
+}  // namespace
+}  // namespace cvh
+
+extern "C" int cvh_paged_attention_fp8_prefill(void* out, const void* q, const uint8_t* k_cache,
+                                               const uint8_t* v_cache, const float* k_scale, const float* v_scale,
+                                               const int64_t* block_tables, int64_t table_width,
+                                               const int64_t* token_seq, const int64_t* token_kv_len,
+                                               int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                               int block_size, int scale_mode, double scale, cvh_stream_t stream) {
+    return cvh::prefill_entry(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq,
+                              token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size, scale_mode, scale,
+                              nullptr, stream);
+}
+
+extern "C" size_t cvh_paged_attention_prefill_workspace_bytes(int64_t num_tokens) {
+    return num_tokens <= 0 ? 0 : cvh::plan_bytes(num_tokens);
+}
+
+extern "C" int cvh_paged_attention_prefill_plan(const int64_t* token_seq, const int64_t* token_kv_len,
+                                                int64_t num_tokens, int64_t table_width, int block_size,
+                                                void* workspace, size_t workspace_bytes, cvh_stream_t stream) {
+    using namespace cvh;
+    if (num_tokens < 0 || table_width < 0) return CVH_ERR_INVALID_ARG;
+    if (num_tokens == 0) return CVH_OK;
+    if (!token_seq || !token_kv_len || !workspace) return CVH_ERR_INVALID_ARG;
+    if (num_tokens > (int64_t{1} << 30)) return CVH_ERR_UNSUPPORTED;
+    const int lg = ilog2_exact(block_size);
+    if (lg < 4 || lg > 12) return CVH_ERR_UNSUPPORTED;
+    if (workspace_bytes < plan_bytes(num_tokens)) return CVH_ERR_WORKSPACE;
+    const int64_t groups = (num_tokens + kWgTok - 1) / kWgTok;
+    int* cost = static_cast<int*>(workspace);
+    prefill_plan_kernel<<<1, kPlanThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+            token_seq, token_kv_len, static_cast<int>(num_tokens), table_width << lg, cost, cost + groups);
+    return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
+}
+
+extern "C" int cvh_paged_attention_fp8_prefill_planned(void* out, const void* q, const uint8_t* k_cache,
+                                                       const uint8_t* v_cache, const float* k_scale,
+                                                       const float* v_scale, const int64_t* block_tables,
+                                                       int64_t table_width, const int64_t* token_seq,
+                                                       const int64_t* token_kv_len, int64_t num_tokens, int n_heads,
+                                                       int n_kv_heads, int head_dim, int block_size, int scale_mode,
+                                                       double scale, const void* workspace, size_t workspace_bytes,
+                                                       cvh_stream_t stream) {
+    using namespace cvh;
+    if (num_tokens > 0 && (!workspace || workspace_bytes < plan_bytes(num_tokens))) return CVH_ERR_WORKSPACE;
+    const int* order = num_tokens > 0 ? static_cast<const int*>(workspace) + (num_tokens + kWgTok - 1) / kWgTok
+                                      : nullptr;
+    return prefill_entry(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_width, token_seq,
+                         token_kv_len, num_tokens, n_heads, n_kv_heads, head_dim, block_size, scale_mode, scale, order,
+                         stream);
 }

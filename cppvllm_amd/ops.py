@@ -112,20 +112,43 @@ def prefill_supported(n_heads: int, n_kv_heads: int, head_dim: int) -> bool:
     return head_dim == 128 and n_heads % n_kv_heads == 0 and n_heads // n_kv_heads in (1, 2)
 
 
+def prefill_workspace(num_tokens: int, device="cuda") -> torch.Tensor:
+    """Workspace of paged_attention_prefill_plan for num_tokens query tokens."""
+    n = int(_lib.lib().cvh_paged_attention_prefill_workspace_bytes(int(num_tokens)))
+    return torch.empty((max(1, (n + 3) // 4),), dtype=torch.int32, device=device)
+
+
+def paged_attention_prefill_plan(token_seq, token_kv_len, table_width: int, block_size: int, workspace) -> None:
+    """Order the 64-token groups of a multi-query batch longest key walk first (once per step)."""
+    T = token_seq.numel()
+    if T == 0:
+        return
+    _require_cuda(token_seq, token_kv_len, workspace)
+    check("paged_attention_prefill_plan", _lib.lib().cvh_paged_attention_prefill_plan(
+        token_seq.data_ptr(), token_kv_len.data_ptr(), T, int(table_width), int(block_size), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(token_seq)))
+
+
 def paged_attention_fp8_prefill(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len,
-                                scale: float) -> None:
+                                scale: float, *, workspace=None) -> None:
     """paged_attention_fp8 for multi-token query rows (chunked prefill) on the MFMA kernel: same
-    arguments and result; no workspace."""
+    arguments and result. workspace: a plan from paged_attention_prefill_plan over the same
+    token_seq / token_kv_len (longest groups first, key tiles split over two half-workgroups)."""
     T = q.size(0)
     if T == 0:
         return
-    _require_cuda(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len)
+    _require_cuda(out, q, k_cache, v_cache, k_scale, v_scale, block_tables, token_seq, token_kv_len, workspace)
     H, HD = q.size(1), q.size(2)
     BS, KV = k_cache.size(1), k_cache.size(2)
-    code = _lib.lib().cvh_paged_attention_fp8_prefill(
-        out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
-        v_scale.data_ptr(), block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(),
-        token_kv_len.data_ptr(), T, H, KV, HD, BS, _scale_mode(k_scale), float(scale), _stream(q))
+    args = (out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
+            v_scale.data_ptr(), block_tables.data_ptr(), block_tables.size(1), token_seq.data_ptr(),
+            token_kv_len.data_ptr(), T, H, KV, HD, BS, _scale_mode(k_scale), float(scale))
+    L = _lib.lib()
+    if workspace is None:
+        code = L.cvh_paged_attention_fp8_prefill(*args, _stream(q))
+    else:
+        code = L.cvh_paged_attention_fp8_prefill_planned(*args, workspace.data_ptr(),
+                                                         workspace.numel() * workspace.element_size(), _stream(q))
     check("paged_attention_fp8_prefill", code)
 
 

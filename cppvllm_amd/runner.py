@@ -157,10 +157,14 @@ class Qwen3:
         # multi-query kernel; decode rows take the stream-K decode kernel
         S = cu_seqlens.numel() - 1
         multi_query = not planned and T >= 2 * S and ops.prefill_supported(H, KV, HD)
+        if multi_query:   # the 64-token groups longest key walk first, once for all layers
+            pws = ops.prefill_workspace(T, dev)
+            ops.paged_attention_prefill_plan(seq, kvl, block_tables.size(1), cache.block_size, pws)
 
         def attention(li, kc, vc, ks, vs):
             if multi_query:
-                ops.paged_attention_fp8_prefill(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale)
+                ops.paged_attention_fp8_prefill(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
+                                                workspace=pws)
             else:
                 ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
                                         workspace=workspace, planned=planned, shared=shared)

@@ -126,6 +126,27 @@ int cvh_paged_attention_fp8_prefill(void* out, const void* q, const uint8_t* k_c
                                     int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim, int block_size,
                                     int scale_mode, double scale, cvh_stream_t stream);
 
+/* Planned multi-query launches. The key walk of a 64-token group grows with its position in its
+ * prompt, so in natural order the longest groups of the last prompts start late and end the
+ * launch. cvh_paged_attention_prefill_plan sorts the groups by their largest (clamped)
+ * token_kv_len, longest first, into the workspace (one 1024-thread workgroup; build it once per
+ * step, stream-ordered before the planned calls, and again when token_seq, token_kv_len or
+ * num_tokens change); cvh_paged_attention_fp8_prefill_planned dispatches (group, kv head) items in
+ * that order, each on 8 waves that split the group's key tiles in two halves and combine their
+ * softmax states in LDS. Same arguments and results as cvh_paged_attention_fp8_prefill (within the
+ * attention tolerance: the two halves change the fp32 summation order); workspace_bytes >=
+ * cvh_paged_attention_prefill_workspace_bytes(num_tokens), else CVH_ERR_WORKSPACE. */
+size_t cvh_paged_attention_prefill_workspace_bytes(int64_t num_tokens);
+int cvh_paged_attention_prefill_plan(const int64_t* token_seq, const int64_t* token_kv_len, int64_t num_tokens,
+                                     int64_t table_width, int block_size, void* workspace, size_t workspace_bytes,
+                                     cvh_stream_t stream);
+int cvh_paged_attention_fp8_prefill_planned(void* out, const void* q, const uint8_t* k_cache, const uint8_t* v_cache,
+                                            const float* k_scale, const float* v_scale, const int64_t* block_tables,
+                                            int64_t table_width, const int64_t* token_seq,
+                                            const int64_t* token_kv_len, int64_t num_tokens, int n_heads,
+                                            int n_kv_heads, int head_dim, int block_size, int scale_mode, double scale,
+                                            const void* workspace, size_t workspace_bytes, cvh_stream_t stream);
+
 /* Planned launches. A decode step runs the same attention layout (block tables, token_seq,
  * token_kv_len, partition count) once per layer; cvh_paged_attention_plan builds, once, what
  * every decode workgroup would otherwise derive at the start of each launch (row prefix, token

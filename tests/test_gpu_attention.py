@@ -20,10 +20,17 @@ DEV = "cuda"
 
 
 def run_gpu(b, partitions=0, prefill=False):
+    """prefill: False (decode kernel), True (multi-query kernel) or "planned" (its planned launch)."""
     out = torch.empty_like(b["q"])
     if prefill:
+        pws = None
+        if prefill == "planned":
+            pws = ops.prefill_workspace(b["q"].shape[0], b["q"].device)
+            ops.paged_attention_prefill_plan(b["token_seq"], b["token_kv_len"], b["block_tables"].shape[1],
+                                             b["block_size"], pws)
         ops.paged_attention_fp8_prefill(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
-                                        b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"])
+                                        b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
+                                        workspace=pws)
     else:
         ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
                                 b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
@@ -458,20 +465,42 @@ def synth_prefill(seed, chunks, BS, H=16, KV=8, per_tensor=False, order="asc"):
     return b
 
 
+PREFILL_MODES = [True, "planned"]
+
+
+@pytest.mark.parametrize("mode", PREFILL_MODES)
 @pytest.mark.parametrize("BS", [16, 32, 256])
 @pytest.mark.parametrize("per_tensor", [False, True])
-def test_prefill_kernel_matches_oracle(orc, BS, per_tensor):
-    say(f"prefill MFMA kernel BS={BS} per_tensor={per_tensor}")
+def test_prefill_kernel_matches_oracle(orc, BS, per_tensor, mode):
+    say(f"prefill MFMA kernel BS={BS} per_tensor={per_tensor} mode={mode}")
     chunks = [(5, 5), (40, 40), (300, 300), (1000, 37), (17, 1), (700, 129), (2, 2)]
     b = synth_prefill(51 + BS, chunks, BS, per_tensor=per_tensor)
-    assert_close_bf16(run_gpu(dev(b), prefill=True), run_oracle(orc, b))
+    assert_close_bf16(run_gpu(dev(b), prefill=mode), run_oracle(orc, b))
 
 
+@pytest.mark.parametrize("mode", PREFILL_MODES)
 @pytest.mark.parametrize("H,KV", [(8, 8), (16, 8), (4, 2), (2, 1), (32, 16)])
-def test_prefill_kernel_head_layouts(orc, H, KV):
-    say(f"prefill MFMA kernel H={H} KV={KV}")
+def test_prefill_kernel_head_layouts(orc, H, KV, mode):
+    say(f"prefill MFMA kernel H={H} KV={KV} mode={mode}")
     b = synth_prefill(61 + H + KV, [(100, 100), (333, 60), (64, 16)], 16, H=H, KV=KV)
-    assert_close_bf16(run_gpu(dev(b), prefill=True), run_oracle(orc, b))
+    assert_close_bf16(run_gpu(dev(b), prefill=mode), run_oracle(orc, b))
+
+
+def test_prefill_plan_orders_groups_longest_first():
+    """The plan is a permutation of the 64-token groups in non-increasing key-tile count."""
+    chunks = [(1024, 1024), (300, 300), (2000, 700), (64, 64), (5, 5)]
+    b = dev(synth_prefill(91, chunks, 16))
+    T = b["q"].shape[0]
+    pws = ops.prefill_workspace(T, DEV)
+    ops.paged_attention_prefill_plan(b["token_seq"], b["token_kv_len"], b["block_tables"].shape[1], 16, pws)
+    torch.cuda.synchronize()
+    G = (T + 63) // 64
+    w = pws.cpu().numpy()
+    order = w[G:2 * G]
+    assert sorted(order.tolist()) == list(range(G))
+    kvl, sq = b["token_kv_len"].cpu().numpy(), b["token_seq"].cpu().numpy()
+    cost = [int(-(-max(kvl[g * 64:(g + 1) * 64][sq[g * 64:(g + 1) * 64] >= 0], default=0) // 32)) for g in range(G)]
+    assert all(cost[order[i]] >= cost[order[i + 1]] for i in range(G - 1))
 
 
 def test_prefill_kernel_rejects_unsupported_gqa():
@@ -481,23 +510,25 @@ def test_prefill_kernel_rejects_unsupported_gqa():
     assert "UNSUPPORTED" in str(e.value)
 
 
-def test_prefill_kernel_ragged_edge_rows(orc):
-    say("prefill MFMA kernel: descending order, decode-like rows, kv_len 0 and padding rows")
+@pytest.mark.parametrize("mode", PREFILL_MODES)
+def test_prefill_kernel_ragged_edge_rows(orc, mode):
+    say(f"prefill MFMA kernel: descending order, decode-like rows, kv_len 0 and padding rows, mode={mode}")
     b = synth_prefill(71, [(50, 50), (9, 1), (10, 1), (400, 3), (33, 33)], 16, order="desc")
     # a padding row (token_seq -1) and a zero-length row: all-zero outputs
     b["token_seq"][3] = -1
     b["token_kv_len"][7] = 0
-    got = run_gpu(dev(b), prefill=True)
+    got = run_gpu(dev(b), prefill=mode)
     want = run_oracle(orc, b)
     assert not got[3].any() and not got[7].any()
     assert_close_bf16(got, want)
 
 
-def test_prefill_kernel_agrees_with_decode_kernel():
-    say("prefill MFMA kernel vs stream-K decode kernel on a 4096-token chunked batch")
+@pytest.mark.parametrize("mode", PREFILL_MODES)
+def test_prefill_kernel_agrees_with_decode_kernel(mode):
+    say(f"prefill MFMA kernel vs stream-K decode kernel on a 4096-token chunked batch, mode={mode}")
     chunks = [(1024, 1024), (2048, 1024), (3000, 1024), (600, 512), (900, 512)]
     b = dev(synth_prefill(81, chunks, 256))
-    assert_close_bf16(run_gpu(b, prefill=True), run_gpu(b), max_abs=1.6e-2, mean_abs=1e-3)
+    assert_close_bf16(run_gpu(b, prefill=mode), run_gpu(b), max_abs=1.6e-2, mean_abs=1e-3)
 
 
 def test_shared_prefix_plan_is_bitwise_identical(orc):
