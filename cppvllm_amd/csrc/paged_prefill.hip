@@ -454,18 +454,29 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const int64_
     const int groups = (T + kWgTok - 1) / kWgTok;
     for (int i = tid; i < kCostBuckets; i += kPlanThreads) hist[i] = 0;
     __syncthreads();
-    for (int gi = tid; gi < groups; gi += kPlanThreads) {
+    // 16 lanes per group, 4 tokens per lane (coalesced), max over the 16 lanes
+    for (int gb = 0; gb < groups; gb += kPlanThreads / 16) {
+        const int gi = gb + (tid >> 4);
         int64_t kmax = 0;
-        for (int j = 0; j < kWgTok; ++j) {
-            const int t = gi * kWgTok + j;
-            if (t >= T) break;
-            const int64_t kv = token_kv_len[t];
-            if (token_seq[t] >= 0 && kv > kmax) kmax = kv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int t = gi * kWgTok + (tid & 15) * 4 + j;
+            if (gi < groups && t < T) {
+                const int64_t kv = token_kv_len[t];
+                if (token_seq[t] >= 0 && kv > kmax) kmax = kv;
+            }
         }
-        kmax = min(kmax, max_keys);
-        const int c = static_cast<int>(min<int64_t>((kmax + kTile - 1) / kTile, kCostBuckets - 1));
-        cost[gi] = c;
-        atomicAdd(&hist[c], 1);
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const int64_t o = __shfl_xor(kmax, d, 64);
+            kmax = o > kmax ? o : kmax;
+        }
+        if (gi < groups && (tid & 15) == 0) {
+            kmax = min(kmax, max_keys);
+            const int c = static_cast<int>(min<int64_t>((kmax + kTile - 1) / kTile, kCostBuckets - 1));
+            cost[gi] = c;
+            atomicAdd(&hist[c], 1);
+        }
     }
     __syncthreads();
     // exclusive scan in descending cost: start[c] = number of groups with cost > c
