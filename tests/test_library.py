@@ -81,6 +81,41 @@ def test_gemm_argument_validation_without_device():
     assert lib.cvh_gemm_bf16_nt_swiglu(p, p, p, 4, 64, 256, 11, None) == unsup         # not a SwiGLU code
 
 
+def test_fused_gemm_and_prefill_plan_argument_validation_without_device():
+    """The fused-epilogue projections and the prefill plan reject bad arguments, unsupported shapes
+    and short workspaces before any device call; their automatic tiles are compiled ones."""
+    lib = _lib.lib()
+    ok, bad, unsup, wsp = _lib.CVH_OK, _lib.CVH_ERR_INVALID_ARG, _lib.CVH_ERR_UNSUPPORTED, _lib.CVH_ERR_WORKSPACE
+    p = C.c_void_p(16)
+    assert lib.cvh_gemm_bf16_nt_residual(None, None, None, None, 0, 1024, 2048, 0, None) == ok
+    assert lib.cvh_gemm_bf16_nt_residual(p, None, p, p, 4, 1024, 2048, 0, None) == bad         # no row_ss
+    assert lib.cvh_gemm_bf16_nt_residual(p, p, p, p, 4, 1000, 2048, 0, None) == unsup          # N % 16
+    assert lib.cvh_gemm_bf16_nt_residual(p, p, p, p, 4, 1024, 2000, 0, None) == unsup          # K % 128
+    assert lib.cvh_gemm_bf16_nt_residual(p, p, p, p, 4, 1024, 2048, 11, None) == unsup         # not a fused tile
+    assert lib.cvh_gemm_bf16_nt_swiglu_rownorm(p, p, p, 1e-6, p, 4, 3072, 1152, 0, None) == unsup  # K % 256
+    assert lib.cvh_gemm_bf16_nt_swiglu_rownorm(p, p, p, 1e-6, p, 4, 3072, 2048, 0, None) == unsup  # K > 1024
+    assert lib.cvh_gemm_bf16_nt_swiglu_rownorm(p, p, None, 1e-6, p, 4, 3072, 1024, 0, None) == bad
+    qkv = lambda *tail: lib.cvh_gemm_qkv_norm_rope_kv_write_fp8(p, p, None, 1e-6, *([p] * 11), *tail)  # noqa: E731
+    assert qkv(0, 1024, 16, 8, 128, 16, 0, 1e-6, 0, None) == ok
+    assert qkv(4, 1024, 16, 8, 64, 16, 0, 1e-6, 0, None) == unsup                             # head_dim 128 only
+    assert qkv(4, 1024, 16, 8, 128, 24, 0, 1e-6, 0, None) == unsup                            # block size
+    assert qkv(4, 1024, 16, 8, 128, 16, 5, 1e-6, 0, None) == unsup                            # scale mode
+    assert qkv(-1, 1024, 16, 8, 128, 16, 0, 1e-6, 0, None) == bad
+    fused = {k: set(_codes(lambda b, n, k=k: lib.cvh_gemm_fused_configs(k, b, n))) for k in range(3)}
+    for M in (1, 15, 16, 64, 65, 128, 129, 256):
+        for k in range(3):
+            assert lib.cvh_gemm_fused_config(k, M) in fused[k], (k, M)
+    assert all(c % 10 * ((c // 100) % 10) * 16 % 128 == 0 for c in fused[2])                 # whole heads
+    # prefill plan: workspace of two int32 per 64-token group
+    assert lib.cvh_paged_attention_prefill_workspace_bytes(0) == 0
+    assert lib.cvh_paged_attention_prefill_workspace_bytes(65) == 2 * 2 * 4
+    assert lib.cvh_paged_attention_prefill_plan(None, None, 0, 4, 16, None, 0, None) == ok
+    assert lib.cvh_paged_attention_prefill_plan(p, p, 100, 4, 16, p, 15, None) == wsp
+    assert lib.cvh_paged_attention_prefill_plan(p, p, 100, 4, 24, p, 16, None) == unsup
+    assert lib.cvh_paged_attention_fp8_prefill_planned(*[p] * 7, 4, p, p, 100, 16, 8, 128, 16, 0, 0.1, p, 15,
+                                                       None) == wsp
+
+
 def _codes(fn):
     n = fn(None, 0)
     buf = (C.c_int * n)()
