@@ -424,7 +424,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(decode attention shards by sequence or kv head with no exchange; see DESIGN.md).",
+              "(decode attention shards by sequence or kv head with no exchange inside the path).",
               file=sys.stderr)
         sys.exit(2)
 

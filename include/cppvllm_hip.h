@@ -167,8 +167,8 @@ int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, c
  * cache policy (the rest non-temporal), so the first sequence to read a shared block leaves it in
  * L2 / the last-level cache for the others. Results are bitwise those of the plain plan and
  * launches; the plain _planned launches ignore the sharing (no per-tile test in their loop).
- * (Serves SURVEY §8(f) prefix-shared reuse; no reference counterpart: the reference re-reads
- *  shared blocks per sequence, engine/block_manager.cpp:80-116 hands out the shared ids.) */
+ * (Prefix-shared block reuse; no reference counterpart: the reference re-reads shared blocks
+ *  per sequence, engine/block_manager.cpp:80-116 hands out the shared ids.) */
 int cvh_paged_attention_plan_shared(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
                                     const int64_t* token_kv_len, const int32_t* shared_blocks, int64_t num_tokens,
                                     int n_heads, int n_kv_heads, int head_dim, int block_size, int partitions,
