@@ -73,16 +73,52 @@ def build_engine(verbose: bool = False) -> Path:
     return ENGINE_LIB
 
 
+SILU_LUT = OBJ_DIR / "silu_bf16_lut.inc"
+
+
+def write_silu_lut(path: Path = SILU_LUT) -> None:
+    """The bf16 SiLU table the kernels index by a gate's 16 bits: silu(g) = g / (1 + exp(-g))
+    in double (the reference's formula, kernels/fused_ops.cu:210-219; exp from the C library,
+    IEEE double division), converted to float, then rounded to bf16 (nearest even; NaN -> quiet
+    NaN with its sign). Generated at build time into the object directory."""
+    import math
+
+    import numpy as np
+    bits = np.arange(65536, dtype=np.uint32)
+    with np.errstate(all="ignore"):
+        g = (bits << 16).view(np.float32).astype(np.float64)
+
+    def c_exp(x: float) -> float:
+        if math.isnan(x):
+            return x
+        try:
+            return math.exp(x)
+        except OverflowError:
+            return math.inf
+    e = np.array([c_exp(-x) for x in g.tolist()], dtype=np.float64)
+    with np.errstate(all="ignore"):
+        s = np.where(np.isnan(g), g, g / (1.0 + e)).astype(np.float32)
+    u = s.view(np.uint32)
+    rne = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    out = np.where((u & 0x7FFFFFFF) > 0x7F800000, (u >> 16) | 0x40, rne).astype(np.uint32)
+    path.parent.mkdir(exist_ok=True)
+    lines = [", ".join(f"0x{int(v):04x}" for v in out[i:i + 16]) + "," for i in range(0, 65536, 16)]
+    tmp = path.with_suffix(".tmp")
+    tmp.write_text("\n".join(lines) + "\n")
+    os.replace(tmp, path)
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source for gfx950 and link the shared library (and the host serving
     core). Returns the HIP library's path."""
     build_engine(verbose)
     hipcc = _hipcc()
     OBJ_DIR.mkdir(exist_ok=True)
+    write_silu_lut()
     objs, cmds = [], []
     for src, extra in SOURCES.items():
         obj = OBJ_DIR / (Path(src).stem + ".o")
-        cmds.append([hipcc, *HIPCC_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *HIPCC_FLAGS, *extra, f"-I{OBJ_DIR}", "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
         if verbose:
             print(" ".join(cmds[-1]))

@@ -189,13 +189,25 @@ __device__ __forceinline__ void norm_row(typename Elem<DT>::T* __restrict__ orow
 // ---- SwiGLU element ---------------------------------------------------------------------------
 // silu(g) * u with the reference's rounding points (kernels/fused_ops.cu:210-219): silu rounded to
 // the storage type, the product left for the caller to round. The exponential is evaluated in
-// double so that the result does not depend on a float exp's last ulp. Shared by the SwiGLU kernel
-// and the gate/up GEMM epilogue, which must agree bit for bit.
+// double so that the result does not depend on a float exp's last ulp. For bf16 the rounded silu
+// depends only on the gate's 16 bits: a 64K-entry table (generated at build time with that double
+// formula, silu_bf16_lut.inc) replaces the ~45 double-precision operations per element. Shared by
+// the SwiGLU kernel and the gate/up GEMM epilogue, which must agree bit for bit.
+namespace {
+__device__ const uint16_t kSiluBf16[65536] = {
+#include "silu_bf16_lut.inc"
+};
+}  // namespace
+
 template <int DT>
 __device__ __forceinline__ float silu_mul(float g, float u) {
-    const double e = exp(-static_cast<double>(g));
-    const float silu = Elem<DT>::load(Elem<DT>::store(static_cast<float>(static_cast<double>(g) / (1.0 + e))));
-    return silu * u;
+    if constexpr (DT == CVH_DTYPE_BF16) {
+        return bf16_bits_to_f32(kSiluBf16[f32_to_bf16_bits(g)]) * u;   // g is a bf16 value
+    } else {
+        const double e = exp(-static_cast<double>(g));
+        const float silu = Elem<DT>::load(Elem<DT>::store(static_cast<float>(static_cast<double>(g) / (1.0 + e))));
+        return silu * u;
+    }
 }
 
 // ---- OCP e4m3fn ------------------------------------------------------------------------------
