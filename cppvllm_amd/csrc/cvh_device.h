@@ -254,6 +254,25 @@ __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v,
 // phase does the arithmetic, so a caller can issue the loads early or overlap several tasks. Shared by the
 // standalone kernel and the QKV-projection epilogue, which must agree bit for bit; callers are
 // built without FMA contraction.
+// P consecutive 16-bit / 8-bit values of a lane as one store (P = 4: 8 / 4 bytes; P = 2: 4 / 2).
+template <int P> __device__ __forceinline__ void store_u16s(uint16_t* dst, const uint32_t (&v)[P]) {
+    if constexpr (P == 4) *reinterpret_cast<uint2*>(dst) = make_uint2(v[0] | (v[1] << 16), v[2] | (v[3] << 16));
+    else *reinterpret_cast<uint32_t*>(dst) = v[0] | (v[1] << 16);
+}
+template <int P> __device__ __forceinline__ void store_u8s(uint8_t* dst, const uint32_t (&v)[P]) {
+    if constexpr (P == 4) *reinterpret_cast<uint32_t*>(dst) = v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24);
+    else *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(v[0] | (v[1] << 8));
+}
+template <int P> __device__ __forceinline__ void load_u16s(const uint16_t* src, uint32_t (&v)[P]) {
+    if constexpr (P == 4) {
+        const uint2 w = *reinterpret_cast<const uint2*>(src);
+        v[0] = w.x & 0xffffu; v[1] = w.x >> 16; v[2] = w.y & 0xffffu; v[3] = w.y >> 16;
+    } else {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
+        v[0] = w & 0xffffu; v[1] = w >> 16;
+    }
+}
+
 struct QkvDst {
     uint16_t* q_out;
     const uint16_t* q_norm;
@@ -281,10 +300,13 @@ template <int HD>
 __device__ __forceinline__ void qkv_task_load_x(QkvTaskIn<HD>& in, const uint16_t* src, int gl) {
     constexpr int HALF = HD / 2, P = HD / 32;
     const int e0 = P * gl;
+    uint32_t lo[P], hi[P];
+    load_u16s<P>(src + e0, lo);
+    load_u16s<P>(src + HALF + e0, hi);
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-        in.x[j] = bf16_bits_to_f32(src[e0 + j]);
-        in.x[P + j] = bf16_bits_to_f32(src[HALF + e0 + j]);
+        in.x[j] = bf16_bits_to_f32(lo[j]);
+        in.x[P + j] = bf16_bits_to_f32(hi[j]);
     }
 }
 // Q/K tasks: the norm gains and this position's cos/sin.
@@ -322,11 +344,14 @@ __device__ __forceinline__ void qkv_task_run(const QkvTaskIn<HD>& in, int64_t t,
         amax = xor_max<16>(amax);
         if (d.v_dense != nullptr) {
             uint16_t* o = d.v_dense + (t * KV + kvh) * HD;
+            uint32_t lo[P], hi[P];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                o[e0 + j] = static_cast<uint16_t>(__float_as_uint(in.x[j]) >> 16);   // the input bits
-                o[HALF + e0 + j] = static_cast<uint16_t>(__float_as_uint(in.x[P + j]) >> 16);
+                lo[j] = __float_as_uint(in.x[j]) >> 16;      // the input bits
+                hi[j] = __float_as_uint(in.x[P + j]) >> 16;
             }
+            store_u16s<P>(o + e0, lo);
+            store_u16s<P>(o + HALF + e0, hi);
         }
         if (slot < 0) return;
         float sc, inv;
@@ -337,11 +362,14 @@ __device__ __forceinline__ void qkv_task_run(const QkvTaskIn<HD>& in, int64_t t,
             inv = 1.0f / d.v_scale[0];
         }
         uint8_t* dst = d.v_cache + (slot * KV + kvh) * HD;
+        uint32_t lo[P], hi[P];
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-            dst[e0 + j] = static_cast<uint8_t>(e4m3_encode(in.x[j] * inv));
-            dst[HALF + e0 + j] = static_cast<uint8_t>(e4m3_encode(in.x[P + j] * inv));
+            lo[j] = e4m3_encode(in.x[j] * inv);
+            hi[j] = e4m3_encode(in.x[P + j] * inv);
         }
+        store_u8s<P>(dst + e0, lo);
+        store_u8s<P>(dst + HALF + e0, hi);
         if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
             if (gl == 0) d.v_scale[(((slot >> d.log2_bs) * KV + kvh) << d.log2_bs) + (slot & bs_mask)] = sc;
         }
@@ -372,11 +400,14 @@ __device__ __forceinline__ void qkv_task_run(const QkvTaskIn<HD>& in, int64_t t,
     }
     if (task < H) {                      // (kernels/fused_ops.cu:168-173)
         uint16_t* dst = d.q_out + (t * H + task) * HD;
+        uint32_t lo[P], hi[P];
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-            dst[e0 + j] = f32_to_bf16_bits(r[j]);
-            dst[HALF + e0 + j] = f32_to_bf16_bits(r[P + j]);
+            lo[j] = f32_to_bf16_bits(r[j]);
+            hi[j] = f32_to_bf16_bits(r[P + j]);
         }
+        store_u16s<P>(dst + e0, lo);
+        store_u16s<P>(dst + HALF + e0, hi);
         return;
     }
 
@@ -388,11 +419,14 @@ __device__ __forceinline__ void qkv_task_run(const QkvTaskIn<HD>& in, int64_t t,
     amax = xor_max<16>(amax);
     if (d.k_dense != nullptr) {
         uint16_t* o = d.k_dense + (t * KV + kvh) * HD;
+        uint32_t lo[P], hi[P];
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-            o[e0 + j] = f32_to_bf16_bits(r[j]);
-            o[HALF + e0 + j] = f32_to_bf16_bits(r[P + j]);
+            lo[j] = f32_to_bf16_bits(r[j]);
+            hi[j] = f32_to_bf16_bits(r[P + j]);
         }
+        store_u16s<P>(o + e0, lo);
+        store_u16s<P>(o + HALF + e0, hi);
     }
     if (slot < 0) return;
     float sc, sinv;
@@ -403,11 +437,14 @@ __device__ __forceinline__ void qkv_task_run(const QkvTaskIn<HD>& in, int64_t t,
         sinv = 1.0f / d.k_scale[0];
     }
     uint8_t* dst = d.k_cache + (slot * KV + kvh) * HD;
+    uint32_t lo[P], hi[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) {
-        dst[e0 + j] = static_cast<uint8_t>(e4m3_encode(r[j] * sinv));
-        dst[HALF + e0 + j] = static_cast<uint8_t>(e4m3_encode(r[P + j] * sinv));
+        lo[j] = e4m3_encode(r[j] * sinv);
+        hi[j] = e4m3_encode(r[P + j] * sinv);
     }
+    store_u8s<P>(dst + e0, lo);
+    store_u8s<P>(dst + HALF + e0, hi);
     if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
         if (gl == 0) d.k_scale[(((slot >> d.log2_bs) * KV + kvh) << d.log2_bs) + (slot & bs_mask)] = sc;
     }
