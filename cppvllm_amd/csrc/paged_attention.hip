@@ -266,7 +266,9 @@ struct Params {
     int num_tokens;
     int n_kv;                // kv heads as the kernel sees them (virtual: physical << kv_shift)
     int kv_shift;            // log2 of the virtual kv heads per physical kv head
-    int wpg;                 // kv heads (waves) per workgroup
+    int wpg;                 // kv heads (waves) per row group
+    int pack;                // row-group ranges per workgroup (wpg * pack waves; 1 unless wpg < 4)
+    int G;                   // tile ranges (workgroups x pack)
     int qrows;               // rows per workgroup whose q is staged in LDS by the prologue
     int log2_bs;
     float q_scale;           // softmax scale * log2(e)
@@ -398,14 +400,20 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // values that are the same for every lane; uniform() makes that visible to the compiler so
     // all the piece bookkeeping below stays in scalar registers
     auto uniform = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
-    const int64_t G = gridDim.x;
-    const int w = blockIdx.x;
+    // A workgroup runs `pack` independent tile ranges of wpg waves each (pack > 1 only for row
+    // groups of one kv head: the hardware spreads a 4-wave workgroup over the 4 SIMDs of a
+    // CU, where one-wave workgroups were seen stacked two deep on some SIMDs while
+    // others of the same CU stayed empty). They share the LDS prefix and token tables (identical
+    // content) and have separate q staging areas.
+    const int64_t G = p.G;
+    // wave-uniform by construction; readfirstlane tells the compiler so (scalar descriptors)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wi = wave % wpg, vg = wave / wpg;
+    const int w = static_cast<int>(blockIdx.x) * p.pack + vg;
     const bool last_wg = (w == G - 1);
     const int lane = threadIdx.x & 63;
     const int grp = lane >> 3;
     const int sub = lane & 7;
-    // wave-uniform by construction; readfirstlane tells the compiler so (scalar descriptors)
-    const int wi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int H = p.n_kv * REP;
     const int log2_bs = p.log2_bs;
     const int kv_shift = p.kv_shift;
@@ -523,8 +531,9 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // block-table round trip before its first K/V load).
     bool preA = false, preB = false, preQ = false;
     int plan_row = -1, plan_lt = 0, plan_rs = -1, plan_re = -1;
-    char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens);
     constexpr int QB = REP * HD * 2;                 // bytes of one row's q slice for one wave
+    char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens) +
+                    static_cast<size_t>(vg) * p.qrows * wpg * QB;
     constexpr int QL = (QB + 1023) / 1024;           // 16-byte loads per lane per row
     if constexpr (PLANNED) {
         // Everything the prologue waits for (q of the first rows, prefix, token metadata) is
@@ -1195,8 +1204,15 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* pla
         rec.r_s = r_s;
         rec.r_e = end_row(pf, rows, u0, u1, r_s);
         rec.U = static_cast<int>(U);
-        // the empty-row pass of the last workgroup may walk trailing empty rows up to `rows`
-        rec.win = rec.r_e - r_s <= kPlanWin - 1 && (w != G - 1 || rows - r_s <= kPlanWin - 1);
+        // the empty-row pass of the last workgroup may walk trailing empty rows up to `rows`; the
+        // ranges packed into one workgroup share the choice (the other path has a barrier)
+        rec.win = 1;
+        for (int v = w - w % p.pack; v < w - w % p.pack + p.pack; ++v) {
+            const int64_t v0 = v * U / G, v1 = (v + 1) * U / G;
+            const int vs = first_row(pf, rows, v0);
+            if (!(end_row(pf, rows, v0, v1, vs) - vs <= kPlanWin - 1 && (v != G - 1 || rows - vs <= kPlanWin - 1)))
+                rec.win = 0;
+        }
         for (int i = 0; i <= kPlanWin; ++i) rec.pre[i] = prefix[min(r_s + i, rows)];
         const int t_s = r_s / hg_count;
         for (int j = 0; j < kPlanWin; ++j) {
@@ -1392,13 +1408,23 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     p.n_kv = n_kv_heads;
     p.kv_shift = kv_shift;
     p.wpg = wpg;
+    p.G = G;
+    // ranges per workgroup: one-wave row groups run 4 (or 2) to a workgroup, as long as that still
+    // leaves a workgroup for every CU (tp = 8 share of config 3: op 27.7 -> 23.3 us per layer;
+    // two-wave row groups measured 3% slower packed and stay one range per workgroup)
+    p.pack = 1;
+    for (int k = wpg == 1 ? 4 : 1; k > 1; k >>= 1)
+        if (G % k == 0 && G / k >= kResidentWaves / 8) {
+            p.pack = k;
+            break;
+        }
     {
         // q staging rows: as many as the LDS left by the row prefix and token table allows
         const size_t fixed = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens));
-        const size_t per_row = static_cast<size_t>(wpg) * rep_v * head_dim * 2;
+        const size_t per_row = static_cast<size_t>(wpg) * p.pack * rep_v * head_dim * 2;
         const int fit = fixed < kLdsBytes ? static_cast<int>((kLdsBytes - fixed) / per_row) : 0;
         if (fit < 1) return CVH_ERR_UNSUPPORTED;
-        p.qrows = std::min(q_stage_rows(wpg, rep_v, head_dim), fit);
+        p.qrows = std::min(q_stage_rows(wpg * p.pack, rep_v, head_dim), fit);
     }
     p.log2_bs = lg;
     // The softmax scale is folded into q with log2(e) (base-2 softmax); a per-tensor K scale is a
@@ -1418,16 +1444,17 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (phase & kPhaseDecode) {
         const int planned = (phase & kPhasePlanned) ? ((phase & kPhaseShared) ? 2 : 1) : 0;
         const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens)) +
-                           static_cast<size_t>(p.qrows) * wpg * rep_v * head_dim * 2;
+                           static_cast<size_t>(p.qrows) * wpg * p.pack * rep_v * head_dim * 2;
+        const int WG = G / p.pack, nth = 64 * wpg * p.pack;
         const bool one_block = (1 << lg) >= kTileKeys;
         bool ok;
         if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
             ok = head_dim == 128
-                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned)
-                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned);
+                         ? launch_decode_rep<128, CVH_SCALE_PER_TOKEN_HEAD>(rep_v, WG, nth, lds, s, p, one_block, planned)
+                         : launch_decode_rep<64, CVH_SCALE_PER_TOKEN_HEAD>(rep_v, WG, nth, lds, s, p, one_block, planned);
         else
-            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned)
-                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep_v, G, 64 * wpg, lds, s, p, one_block, planned);
+            ok = head_dim == 128 ? launch_decode_rep<128, CVH_SCALE_PER_TENSOR>(rep_v, WG, nth, lds, s, p, one_block, planned)
+                                 : launch_decode_rep<64, CVH_SCALE_PER_TENSOR>(rep_v, WG, nth, lds, s, p, one_block, planned);
         if (!ok) return CVH_ERR_UNSUPPORTED;
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }

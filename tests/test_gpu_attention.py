@@ -377,6 +377,24 @@ def test_planned_equals_unplanned_bitwise(name):
     assert np.array_equal(run_planned(db, parts), run_gpu(db, parts))
 
 
+@pytest.mark.parametrize("parts", [0, 1028, 514, 1030, 1024])
+def test_one_kv_head_packed_workgroups(orc, parts):
+    """One kv head per row group: the launch runs 4 (or 2) tile ranges per workgroup when that
+    leaves a workgroup per CU (automatic 1024 partitions -> 4; 1028 -> 4; 514, 1030 -> 2). Planned
+    and unplanned launches agree bitwise, empty rows stay zero and sampled rows match the oracle."""
+    say(f"one kv head, packed ranges, partitions {parts}")
+    rng = np.random.default_rng(67)
+    lens = [int(x) for x in rng.integers(1, 1400, size=200)]
+    b = synth(67, lens, 16, H=2, KV=1)
+    b["token_kv_len"][::17] = 0
+    db = dev(b)
+    got = run_gpu(db, parts)
+    assert np.array_equal(run_planned(db, parts), got)
+    assert not got[::17].any()
+    rows = np.arange(1, 200, 13)
+    assert_close_bf16(got[rows], run_oracle(orc, b, rows))
+
+
 def test_plan_shared_by_layers_config3(orc):
     # one plan, two layers with different caches (the decode-step pattern); each equals the
     # unplanned call bitwise, and layer 0 matches the oracle
