@@ -50,6 +50,17 @@ constexpr int kVtStride = 34;      // bf16 per LDS row of V^T
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kNegHuge = -1e30f;
 
+// K/V and scale tiles are read with raw buffer loads: a scalar descriptor per wave and tile (the
+// block's first key of the tile as base, the valid keys as size) and per-thread offsets fixed for
+// the whole launch, so addressing costs no vector instructions and keys past the context (or in
+// a block whose table entry is negative) read as zeros without a branch.
+constexpr int kBufWord3 = 0x00020000;      // raw buffer, 32-bit data format
+constexpr int kNt = 2;                     // non-temporal: each K/V byte is read once per workgroup
+typedef unsigned int u32x4_p __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufWord3);
+}
+
 template <bool HI> __device__ __forceinline__ uint32_t pk_bf16(uint32_t w) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
 }
@@ -91,7 +102,8 @@ struct PrefillLds {
 
 // The workgroup's share of one tile as loaded by thread tid (raw e4m3 and f32 scales):
 // K: key tid/8, bytes (tid%8)*16 .. +16;  V: keys 4*(tid/32) + e, bytes 4*(tid%32) .. +4;
-// scales: key tid (tid < 32).
+// scales: key tid/8. Every wave's keys lie in one half of the tile (wave w: keys 8w .. 8w+7),
+// so with 16-key blocks each wave still reads from a single block.
 struct TileRegs {
     uint4 k;
     uint32_t v[4];
@@ -168,6 +180,13 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     const int all_kvl = smv[0].tkvl[lane];
     const int64_t my_seq = smv[0].tseq[16 * w + i16];
     const int my_kvl = smv[0].tkvl[16 * w + i16];
+    // this wave's keys: [8w, 8w + 8) of every tile; with 16-key blocks waves 2, 3 read the second block
+    const int khalf = (BS < kTile && w >= 2) ? 16 : 0;
+    const int khalf_span = BS < kTile ? 16 : kTile;
+    const uint32_t row_bytes32 = static_cast<uint32_t>(row_bytes);
+    const uint32_t k_off = static_cast<uint32_t>((tid >> 3) - khalf) * row_bytes32 + kvh * kHD + (tid & 7) * 16;
+    const uint32_t v_off = static_cast<uint32_t>(4 * (tid >> 5) - khalf) * row_bytes32 + kvh * kHD + (tid & 31) * 4;
+    const uint32_t s_off = static_cast<uint32_t>((tid >> 3) - khalf) * 4u;
     uint64_t todo = __builtin_amdgcn_ballot_w64(all_kvl > 0);
     while (todo) {
         const int leader = __builtin_ctzll(todo);
@@ -192,46 +211,36 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
         for (int d = 1; d < 16; d <<= 1) wk = max(wk, __shfl_xor(wk, d, 64));
         const int wave_kmax = __builtin_amdgcn_readfirstlane(wk);
+        // tiles below every row's length need no causal mask (rows outside the run have length 0)
+        int wn = row_kvl;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) wn = min(wn, __shfl_xor(wn, d, 64));
+        const int wave_kmin = __builtin_amdgcn_readfirstlane(wn);
 
-        // cooperative load of tile kb0 into registers (keys >= kmax and negative table entries
+        // cooperative load of tile kb0 into registers (keys >= kend and negative table entries
         // read as zeros; a negative entry inside a context is invalid input)
         auto load_tile = [&](int kb0, TileRegs& r) {
-            const bool any = kb0 < kend;
-            const int64_t blk0 = any ? trow[kb0 >> lg_bs] : -1;
-            const int64_t blk1 = BS < kTile ? (kb0 + 16 < kend ? trow[(kb0 + 16) >> lg_bs] : -1) : blk0;
-            auto slot_of = [&](int key, bool& ok) -> int64_t {
-                const int64_t b = (BS < kTile && key >= 16) ? blk1 : blk0;
-                ok = b >= 0 && kb0 + key < kend;
-                return (b << lg_bs) + ((kb0 + key) & bs_mask);
-            };
-            bool ok;
-            {
-                const int key = tid >> 3, cc = tid & 7;
-                const int64_t sl = slot_of(key, ok);
-                r.k = ok ? *reinterpret_cast<const uint4*>(kc + sl * row_bytes + kvh * kHD + cc * 16)
-                         : make_uint4(0, 0, 0, 0);
-            }
-            {
-                const int kg = tid >> 5, c = tid & 31;
+            const int kfirst = kb0 + khalf;                       // first key of this wave's block range
+            const int span = min(max(kend - kfirst, 0), khalf_span);
+            const int64_t blk = span > 0 ? trow[kfirst >> lg_bs] : -1;
+            const int valid = blk >= 0 ? span : 0;
+            const int64_t slot0 = (blk << lg_bs) + (kfirst & bs_mask);
+            const uint32_t vb = static_cast<uint32_t>(valid) * static_cast<uint32_t>(row_bytes);
+            const auto rk = rsrc(kc + slot0 * row_bytes, vb);
+            const auto rv = rsrc(vc + slot0 * row_bytes, vb);
+            const u32x4_p kw = __builtin_amdgcn_raw_buffer_load_b128(rk, k_off, 0, kNt);
+            r.k = make_uint4(kw[0], kw[1], kw[2], kw[3]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int64_t sl = slot_of(4 * kg + e, ok);
-                    r.v[e] = ok ? *reinterpret_cast<const uint32_t*>(vc + sl * row_bytes + kvh * kHD + c * 4) : 0u;
-                }
-            }
-            r.ks = r.vs = 0.f;
-            if (tid < kTile) {
-                const int64_t sl = slot_of(tid, ok);
-                if (ok) {
-                    if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
-                        const int64_t si = (((sl >> lg_bs) * KV + kvh) << lg_bs) + (sl & bs_mask);
-                        r.ks = ksc[si];
-                        r.vs = vsc[si];
-                    } else {
-                        r.ks = ks_tensor;
-                        r.vs = vs_tensor;
-                    }
-                }
+            for (int e = 0; e < 4; ++e)
+                r.v[e] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rv, v_off + e * row_bytes32, 0, kNt));
+            if constexpr (SCALE_MODE == CVH_SCALE_PER_TOKEN_HEAD) {
+                const int64_t si = ((((blk < 0 ? 0 : blk) * KV + kvh)) << lg_bs) + (kfirst & bs_mask);
+                r.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(ksc + si, valid * 4u), s_off, 0, kNt));
+                r.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc(vsc + si, valid * 4u), s_off, 0, kNt));
+            } else {
+                const bool ok = s_off < valid * 4u;
+                r.ks = ok ? ks_tensor : 0.f;
+                r.vs = ok ? vs_tensor : 0.f;
             }
         };
         // registers -> LDS buffer: K converted to bf16, V transposed (4x4 byte blocks with
@@ -264,12 +273,12 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                     dst[1] = pk_bf16<true>(tr[e]);
                 }
             }
-            if (tid < kTile) {
-                sm.ks[buf][tid] = r.ks * scale_log2;
-                sm.vs[buf][tid] = r.vs;
+            if ((tid & 7) == 0) {
+                sm.ks[buf][tid >> 3] = r.ks * scale_log2;
+                sm.vs[buf][tid >> 3] = r.vs;
             }
         };
-        auto compute = [&](int buf, int kb0) {
+        auto compute = [&](int buf, int kb0, bool masked) {
             f32x4_t sc[2][REP];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -297,16 +306,22 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
             }
 #pragma unroll
             for (int rb = 0; rb < REP; ++rb) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sc[kb][rb][r] *= ksr[kb][r];
+                if (masked) {              // wave-uniform: only tiles reaching past a row's length
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (kb0 + kb * 16 + g * 4 + r >= row_kvl) sc[kb][rb][r] = -INFINITY;
+                }
                 float mt = kNegHuge;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int key = kb0 + kb * 16 + g * 4 + r;
-                        const float sv = key < row_kvl ? sc[kb][rb][r] * ksr[kb][r] : -INFINITY;
-                        sc[kb][rb][r] = sv;
-                        mt = fmaxf(mt, sv);
-                    }
+                    for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[kb][rb][r]);
                 mt = max_groups(mt);
                 const float mn = fmaxf(m[rb], mt);
                 const float alpha = __builtin_amdgcn_exp2f(m[rb] - mn);
@@ -347,7 +362,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
         __syncthreads();
         for (int i = 0, kb0 = kbeg; i < n0; ++i, kb0 += kTile) {
             const int buf = i & 1;
-            if (kb0 < kend && kb0 < wave_kmax) compute(buf, kb0);
+            if (kb0 < kend && kb0 < wave_kmax) compute(buf, kb0, kb0 + kTile > wave_kmin);
             if (kb0 + kTile < kend) {
                 store_tile(buf ^ 1, rg);
                 load_tile(kb0 + 2 * kTile, rg);
