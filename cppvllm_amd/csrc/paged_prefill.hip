@@ -42,13 +42,14 @@ constexpr int kHD = 128;
 constexpr int kQTok = 16;          // query tokens per wave
 constexpr int kTile = 32;          // keys per tile
 // LDS row strides chosen against bank conflicts (64 banks of 4 bytes):
-//  * V^T rows are 17 dwords (32 keys + 2 pad bf16): the writers (lane c -> row 4c + e) land on
-//    banks 4*17*c mod 64, 16 distinct 2-dword slots per 16 lanes; accessed as dword pairs
-//    (ds_write2/ds_read2_b32), since odd rows are only 4-byte aligned;
+//  * V^T rows are 18 dwords (32 keys + 4 pad bf16), 8-byte aligned, so a lane's 16 fragment
+//    reads are ds_read_b64 at immediate offsets from one address (rows j*16 + i16 lie
+//    j * 1152 bytes apart); the 16 rows read together land on distinct even banks;
 //  * K rows are 136 bf16 (272 bytes): the 16 rows read by one 16-byte load land 4 banks apart.
-constexpr int kVtStride = 34;      // bf16 per LDS row of V^T
+constexpr int kVtStride = 36;      // bf16 per LDS row of V^T
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kNegHuge = -1e30f;
+constexpr float kRescaleLog2 = 8.0f;   // tolerated staleness of the running max (log2 units)
 
 // K/V and scale tiles are read with raw buffer loads: a scalar descriptor per wave and tile (the
 // block's first key of the tile as base, the valid keys as size) and per-thread offsets fixed for
@@ -323,7 +324,10 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
                     for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[kb][rb][r]);
                 mt = max_groups(mt);
-                const float mn = fmaxf(m[rb], mt);
+                // the running max only moves when the tile's max exceeds it by more than 2^8 (a
+                // stale max leaves p <= 2^8: exact in fp32, the same relative bf16 rounding), so
+                // most tiles skip the rescale of O
+                const float mn = mt > m[rb] + kRescaleLog2 ? mt : m[rb];
                 const float alpha = __builtin_amdgcn_exp2f(m[rb] - mn);
                 m[rb] = mn;
                 float ps = 0.f;
@@ -346,7 +350,8 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t* v32 = reinterpret_cast<const uint32_t*>(&sm.vt[buf][(j * 16 + i16) * kVtStride + g * 4]);
-                    const uint32_t va[4] = {v32[0], v32[1], v32[8], v32[9]};
+                    const uint2 lo = *reinterpret_cast<const uint2*>(v32), hi = *reinterpret_cast<const uint2*>(v32 + 8);
+                    const uint32_t va[4] = {lo.x, lo.y, hi.x, hi.y};
                     o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pop,
                                                                        o[rb][j], 0, 0, 0);
                 }
