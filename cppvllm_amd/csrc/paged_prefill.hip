@@ -122,6 +122,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
         const int* __restrict__ order) {
     constexpr int NH = KSPLIT ? 2 : 1;
     __shared__ __align__(16) PrefillLds smv[NH];
+    __shared__ int half_sync[2];
     const int tid = threadIdx.x & 255, lane = tid & 63;
     const int half = KSPLIT ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 8) : 0;
     PrefillLds& sm = smv[half];
@@ -135,6 +136,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     const int BS = 1 << lg_bs, bs_mask = BS - 1;
     const int64_t row_bytes = static_cast<int64_t>(KV) * kHD;      // one slot row, all kv heads
 
+    if (threadIdx.x < 2) half_sync[threadIdx.x] = 0;
     // token metadata of the 64 tokens -> LDS (clamped like the decode kernel)
     if (half == 0 && tid < kWgTok) {
         const int t = t0 + tid;
@@ -188,6 +190,27 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     const uint32_t k_off = static_cast<uint32_t>((tid >> 3) - khalf) * row_bytes32 + kvh * kHD + (tid & 7) * 16;
     const uint32_t v_off = static_cast<uint32_t>(4 * (tid >> 5) - khalf) * row_bytes32 + kvh * kHD + (tid & 31) * 4;
     const uint32_t s_off = static_cast<uint32_t>((tid >> 3) - khalf) * 4u;
+    // The 4 waves sharing a tile buffer synchronise per tile. With two halves this is a counter in
+    // LDS per half instead of the workgroup barrier, so the halves run their own tile counts and
+    // drift apart: the two waves of a SIMD then tend to be in different phases (one issuing MFMA,
+    // the other softmax VALU). The wait is bounded (a lost wave cannot hang the launch).
+    int passed = 0;
+    auto tile_barrier = [&]() {
+        if constexpr (!KSPLIT) {
+            __syncthreads();
+        } else {
+            ++passed;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) __hip_atomic_fetch_add(&half_sync[half], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            for (int spin = 0; spin < (1 << 22); ++spin) {
+                const int c = __builtin_amdgcn_readfirstlane(
+                        __hip_atomic_load(&half_sync[half], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (c >= 4 * passed) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        }
+    };
     uint64_t todo = __builtin_amdgcn_ballot_w64(all_kvl > 0);
     while (todo) {
         const int leader = __builtin_ctzll(todo);
@@ -200,9 +223,10 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) kmax_l = max(kmax_l, __shfl_xor(kmax_l, d, 64));
         const int kmax = __builtin_amdgcn_readfirstlane(kmax_l);
-        // this half's key range: tiles [0, n0) or [n0, ntiles); both halves run n0 iterations
+        // this half's key range: tiles [0, n0) or [n0, ntiles)
         const int ntiles = (kmax + kTile - 1) / kTile;
         const int n0 = KSPLIT ? (ntiles + 1) >> 1 : ntiles;
+        const int n_iter = half ? ntiles - n0 : n0;
         const int kbeg = half ? n0 * kTile : 0;
         const int kend = half ? kmax : min(kmax, n0 * kTile);
         const int64_t* trow = tables + rseq * W;
@@ -364,15 +388,15 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
         load_tile(kbeg, rg);
         store_tile(0, rg);
         load_tile(kbeg + kTile, rg);
-        __syncthreads();
-        for (int i = 0, kb0 = kbeg; i < n0; ++i, kb0 += kTile) {
+        tile_barrier();
+        for (int i = 0, kb0 = kbeg; i < n_iter; ++i, kb0 += kTile) {
             const int buf = i & 1;
             if (kb0 < kend && kb0 < wave_kmax) compute(buf, kb0, kb0 + kTile > wave_kmin);
             if (kb0 + kTile < kend) {
                 store_tile(buf ^ 1, rg);
                 load_tile(kb0 + 2 * kTile, rg);
             }
-            __syncthreads();
+            tile_barrier();
         }
     }
 
@@ -381,6 +405,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
         constexpr int kVals = 2 + 32;
         static_assert(sizeof(smv) >= REP * kVals * 256 * sizeof(float), "combine buffer");
         float* xs = reinterpret_cast<float*>(smv);
+        __syncthreads();                 // both halves are done with their tiles
         if (half) {
 #pragma unroll
             for (int rb = 0; rb < REP; ++rb) {
