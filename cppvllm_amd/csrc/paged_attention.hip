@@ -780,7 +780,10 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                     for (int j = 0; j < 8; ++j) om[j][r] *= cr;
                 }
             }
-            uint32_t pw[4];
+            // p (with the V scale) as a bf16 pair hi + lo: hi = bf16(w), lo = bf16(w - hi), so the two
+            // PV products carry w to ~16 significant bits (the fp32 weights of the VALU path; a
+            // single bf16 rounding of w lets 20x-outlier rows drift by several output ulps)
+            uint32_t pw[4], pl[4];
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const float vsr[4] = {row_bcast<0>(tl.vs[kb]), row_bcast<1>(tl.vs[kb]), row_bcast<2>(tl.vs[kb]),
@@ -792,10 +795,13 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                     lm += p0v + p1v;
                     const float w0 = (SM == CVH_SCALE_PER_TOKEN_HEAD) ? p0v * vsr[r] : p0v;
                     const float w1 = (SM == CVH_SCALE_PER_TOKEN_HEAD) ? p1v * vsr[r + 1] : p1v;
-                    pw[kb * 2 + r / 2] = pack_bf16x2_rne(w0, w1);
+                    const uint32_t h = pack_bf16x2_rne(w0, w1);
+                    pw[kb * 2 + r / 2] = h;
+                    pl[kb * 2 + r / 2] = pack_bf16x2_rne(w0 - __uint_as_float(h << 16), w1 - __uint_as_float(h & 0xffff0000u));
                 }
             }
             const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+            const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, make_uint4(pl[0], pl[1], pl[2], pl[3]));
 #pragma unroll
             for (int hw = 0; hw < 2; ++hw) {        // d = 8*i16 + 4*hw + jj
                 uint32_t t0[4], t1[4];
@@ -806,9 +812,11 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 transpose4x4(w0, t0);               // t0[jj]: keys 4g..4g+3 at d = 8*i16 + 4*hw + jj
                 transpose4x4(w1, t1);               // t1[jj]: keys 16+4g..
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-                    om[4 * hw + jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, fp8x8_bf16(t0[jj], t1[jj]),
-                                                                            om[4 * hw + jj], 0, 0, 0);
+                for (int jj = 0; jj < 4; ++jj) {
+                    const bf16x8_t vb = fp8x8_bf16(t0[jj], t1[jj]);
+                    om[4 * hw + jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, om[4 * hw + jj], 0, 0, 0);
+                    om[4 * hw + jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, vb, om[4 * hw + jj], 0, 0, 0);
+                }
             }
         } else {
         float sc[REP][kSteps];

@@ -6,10 +6,10 @@
 // query heads share the kv head, K/V dequantised with per-(token, kv head) (or per-tensor)
 // scales, softmax in fp32. The decode kernel walks one query token per row; here 16 consecutive
 // query tokens of a sequence share every K/V tile, so the score and PV products are real dense
-// contractions and run on MFMA (v_mfma_f32_16x16x32_bf16):
+// contractions and run on MFMA (v_mfma_f32_16x16x32_bf16 for scores, _f16 for PV):
 //
 //   S^T[key][row] = K . Q^T   A = K   (16 keys x 32 d, e4m3 -> bf16 exact),  B = Q^T (bf16)
-//   O^T[d][row]  += V^T . P^T A = V^T (16 d x 32 keys, bf16 via LDS),        B = P^T (bf16, v scale folded)
+//   O^T[d][row]  += V^T . P^T A = V^T (16 d x 32 keys, fp16 via LDS),        B = P^T (fp16, v scale folded)
 //
 // Both products put one query row per lane column (lane % 16), so the row's softmax state, its
 // causal mask and its output accumulators live in the same lanes with no cross-lane shuffles
@@ -20,7 +20,7 @@
 //
 // Work: a workgroup = (64 consecutive query tokens, one kv head), 4 waves of 16 tokens each
 // (REP query heads per token), walking the keys of the tokens' sequence in 32-key tiles. The 256
-// threads load each tile once for all four waves: K is converted to bf16 and V transposed
+// threads load each tile once for all four waves: K is converted to bf16 and V transposed to fp16
 // (each thread loads a 4 key x 4 d byte block with dword loads, transposes it with v_perm_b32 and
 // converts it) into a double-buffered LDS tile, so one tile is multiplied while the next sits in
 // registers and the one after is in flight. Tokens of different sequences inside the 64 run as
@@ -70,6 +70,18 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 // two floats -> packed bf16 pair, round to nearest even (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_p));
+}
+
+// The PV product runs in fp16: V e4m3 -> fp16 is exact (like bf16), and p (times the V scale,
+// <= 2^8 x the scale) keeps 11 significant bits instead of bf16's 8, so a row dominated by a few
+// 20x-outlier values stays within an output ulp of the fp32 restatement.
+typedef _Float16 f16x2_p __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+template <bool HI> __device__ __forceinline__ uint32_t pk_f16(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_p));
 }
 
 // max / sum over the 4 lane groups (lanes l, l^16, l^32, l^48), xor 16 then xor 32, with the
@@ -268,7 +280,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                 r.vs = ok ? vs_tensor : 0.f;
             }
         };
-        // registers -> LDS buffer: K converted to bf16, V transposed (4x4 byte blocks with
+        // registers -> LDS buffer: K converted to bf16, V transposed to fp16 (4x4 byte blocks with
         // v_perm_b32) and converted, scales
         auto store_tile = [&](int buf, const TileRegs& r) {
             {
@@ -294,8 +306,8 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.vt[buf][(c * 4 + e) * kVtStride + 4 * kg]);
-                    dst[0] = pk_bf16<false>(tr[e]);
-                    dst[1] = pk_bf16<true>(tr[e]);
+                    dst[0] = pk_f16<false>(tr[e]);
+                    dst[1] = pk_f16<true>(tr[e]);
                 }
             }
             if ((tid & 7) == 0) {
@@ -363,21 +375,21 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                         const float p0 = __builtin_amdgcn_exp2f(sc[kb][rb][r] - mn);
                         const float p1 = __builtin_amdgcn_exp2f(sc[kb][rb][r + 1] - mn);
                         ps += p0 + p1;
-                        pp[kb * 2 + r / 2] = pack_bf16x2(p0 * vsr[kb][r], p1 * vsr[kb][r + 1]);
+                        pp[kb * 2 + r / 2] = pack_f16x2(p0 * vsr[kb][r], p1 * vsr[kb][r + 1]);
                     }
                 lsum[rb] = lsum[rb] * alpha + ps;
                 if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {     // wave-uniform: the max moved
 #pragma unroll
                     for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
                 }
-                const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pp);
+                const f16x8_t pop = __builtin_bit_cast(f16x8_t, pp);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t* v32 = reinterpret_cast<const uint32_t*>(&sm.vt[buf][(j * 16 + i16) * kVtStride + g * 4]);
                     const uint2 lo = *reinterpret_cast<const uint2*>(v32), hi = *reinterpret_cast<const uint2*>(v32 + 8);
                     const uint32_t va[4] = {lo.x, lo.y, hi.x, hi.y};
-                    o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va), pop,
-                                                                       o[rb][j], 0, 0, 0);
+                    o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, va), pop,
+                                                                      o[rb][j], 0, 0, 0);
                 }
             }
         };

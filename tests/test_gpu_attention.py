@@ -182,6 +182,20 @@ def test_gqa_mfma_config3_and_planned(orc, H):
         assert_close_bf16(mine, two, max_abs=1.6e-2, mean_abs=1e-3)
 
 
+@pytest.mark.parametrize("H", [32, 64])
+def test_gqa_mfma_config4_outliers(orc, H):
+    """GQA 4 / 8 on the MFMA path over config 4 (contexts to 32k keys, 20x outliers): all 64 rows
+    against the oracle. The outputs reach |x| ~ 60, so the bar is the one-ulp floor of
+    test_config4_long_context; the PV weights must carry more than one bf16 rounding for it."""
+    say(f"GQA MFMA config 4 H={H}")
+    b = workloads.config4(device="cpu")
+    g = torch.Generator().manual_seed(H)
+    b["n_heads"] = H
+    b["q"] = torch.randn((b["q"].shape[0], H, 128), generator=g).to(torch.bfloat16)
+    got = run_gpu(dev(b))
+    assert_close_bf16(got, run_oracle(orc, b), ulp_floor=True)
+
+
 def test_empty_context_rows_are_zero(orc):
     say("kv_len 0 rows")
     b = synth(5, [100, 50], 16)
@@ -502,6 +516,26 @@ def test_prefill_kernel_head_layouts(orc, H, KV, mode):
     say(f"prefill MFMA kernel H={H} KV={KV} mode={mode}")
     b = synth_prefill(61 + H + KV, [(100, 100), (333, 60), (64, 16)], 16, H=H, KV=KV)
     assert_close_bf16(run_gpu(dev(b), prefill=mode), run_oracle(orc, b))
+
+
+@pytest.mark.parametrize("mode", PREFILL_MODES)
+def test_prefill_kernel_outlier_rows(orc, mode):
+    """Chunked-prefill rows (the last 96 positions of 4 sequences, contexts to 5000) over a cache
+    with config 4's 1% of 20x outliers: all rows against the oracle at the one-ulp floor (outputs
+    reach |x| ~ 30, where the PV weights need more than bf16's 8 significant bits)."""
+    say(f"prefill rows over outlier K/V, mode {mode}")
+    lens = [3000, 1500, 800, 5000]
+    b = workloads.decode_batch(lens, 256, 77, "cpu", outlier_frac=0.01)
+    tseq, tlen = [], []
+    for i, L in enumerate(lens):
+        for j in range(96):
+            tseq.append(i)
+            tlen.append(L - 95 + j)
+    b["token_seq"] = torch.tensor(tseq, dtype=torch.int64)
+    b["token_kv_len"] = torch.tensor(tlen, dtype=torch.int64)
+    b["q"] = torch.randn((len(tseq), 16, 128), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    got = run_gpu(dev(b), prefill=mode)
+    assert_close_bf16(got, run_oracle(orc, b), ulp_floor=True)
 
 
 def test_prefill_plan_orders_groups_longest_first():
