@@ -41,6 +41,36 @@ def test_rms_norm_bitexact_shapes(orc, N, D):
     assert np.array_equal(bits(out), orc.rms_norm(np_(x), np_(wt), 1e-6))
 
 
+def test_norm_special_rows_bitexact(orc):
+    """rms_norm / add_rms_norm on rows at the edges of fp32 sum-of-squares arithmetic, bit-exact:
+    zeros (eps only), 1e-20 (squares underflow), 1e19 (the sum overflows to inf: the row maps to
+    zero), a single huge element among ordinary ones, and bf16's largest finite value."""
+    say("rms_norm special rows")
+    g = torch.Generator().manual_seed(99)
+    D = 1024
+    x = torch.randn((8, D), generator=g)
+    x[0] = 0.0
+    x[1] *= 1e-20
+    x[2] = 1e19
+    x[3, 17] = 1e18
+    x[4] = 3.38e38
+    x[5, ::2] = 0.0
+    xb = x.to(torch.bfloat16)
+    wt = (torch.rand((D,), generator=g) + 0.5).to(torch.bfloat16)
+    out = torch.empty((8, D), dtype=torch.bfloat16, device=DEV)
+    ops.fused.rms_norm(out, xb.to(DEV), wt.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out), orc.rms_norm(np_(xb), np_(wt), 1e-6))
+    r = torch.randn((8, D), generator=g).to(torch.bfloat16)
+    rd = r.to(DEV)
+    out2 = torch.empty_like(out)
+    ops.fused.add_rms_norm(rd, xb.to(DEV), wt.to(DEV), out2, 1e-6)
+    torch.cuda.synchronize()
+    r_want, o_want = orc.add_rms_norm(np_(r), np_(xb), np_(wt), 1e-6)
+    assert np.array_equal(bits(rd), r_want)
+    assert np.array_equal(bits(out2), o_want)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_norm_other_dtypes_bitexact(orc, dtype):
     say(f"add_rms_norm dtype={dtype}")
@@ -124,6 +154,37 @@ def test_qk_norm_rope_head_dim_64(orc):
     }
     w["slots"][::7] = -1
     _run_qkv(orc, w, HD, BS, per_tensor=False, dense=True, nb=nb)
+
+
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_qk_norm_rope_kv_write_special_rows(orc, per_tensor):
+    """Rows that exercise the edges of the scale and norm arithmetic, bit-exact against the oracle:
+    an all-zero V head (amax 0: the 1e-8 scale floor), an all-zero K head (RMS of zeros: eps
+    only), V at 1e4 and at 1e-30 (bf16 subnormal range), one V value near the bf16 maximum (every
+    other code of the head flushes to zero), q at 1e-20, and with per-tensor scales V values far
+    beyond 448 x scale (saturation to +-448)."""
+    say(f"qk_norm_rope_kv_write special rows per_tensor={per_tensor}")
+    g = torch.Generator().manual_seed(4242)
+    T, H, KV, HD, BS = 64, 16, 8, 128, 16
+    nb = math.ceil(T / BS) + 1
+    qkv = torch.randn((T, (H + 2 * KV) * HD), generator=g)
+    v0 = (H + KV) * HD                                   # first V column
+    qkv[3, v0:v0 + HD] = 0.0                             # V head 0 of token 3: all zero
+    qkv[7, H * HD:H * HD + HD] = 0.0                     # K head 0 of token 7: all zero
+    qkv[5, v0:] *= 1e4
+    qkv[6, v0:] *= 1e-30
+    qkv[11, v0 + 5] = 3.0e38
+    qkv[9, :H * HD] *= 1e-20
+    qkv[13, v0:] *= 300.0                                # with per-tensor scale 0.007: |v| / s >> 448
+    w = {
+        "n_heads": H, "n_kv_heads": KV, "max_position": 40960,
+        "qkv": qkv.to(torch.bfloat16),
+        "q_norm": (torch.rand((HD,), generator=g) + 0.5).to(torch.bfloat16),
+        "k_norm": (torch.rand((HD,), generator=g) + 0.5).to(torch.bfloat16),
+        "positions": torch.randint(0, 40960, (T,), generator=g),
+        "slots": torch.randperm(nb * BS, generator=g)[:T],
+    }
+    _run_qkv(orc, w, HD, BS, per_tensor=per_tensor, dense=True, nb=nb)
 
 
 def test_fp8_quantize_matches_oracle(orc):
