@@ -139,10 +139,13 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     const int half = KSPLIT ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 8) : 0;
     PrefillLds& sm = smv[half];
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // item = (64-token group, kv head): blockIdx.x walks the groups of kv head blockIdx.y, or with
-    // a plan, 1-D blockIdx.x walks order[] (groups by descending key-tile count) x kv heads
-    const int item_group = order ? order[blockIdx.x / KV] : static_cast<int>(blockIdx.x);
-    const int kvh = order ? static_cast<int>(blockIdx.x % KV) : static_cast<int>(blockIdx.y);
+    // item = (64-token group, kv head), kv heads fastest along the 1-D grid. With a plan the groups
+    // come from order[] (descending key-tile count); without one they run last group first: a
+    // prompt's later groups attend over more keys, so this starts the long items of each prompt
+    // early (4096-token step of config-5 prompts: 46.1 -> 41.8 us against first group first)
+    const int item_group = order ? order[blockIdx.x / KV]
+                                 : static_cast<int>(gridDim.x) / KV - 1 - static_cast<int>(blockIdx.x) / KV;
+    const int kvh = static_cast<int>(blockIdx.x) % KV;
     const int t0 = item_group * kWgTok;
     const int g = lane >> 4, i16 = lane & 15;
     const int BS = 1 << lg_bs, bs_mask = BS - 1;
@@ -487,7 +490,7 @@ int launch_rep(uint16_t* out, const uint16_t* q, const uint8_t* kc, const uint8_
         paged_prefill_kernel<REP, SM, true><<<dim3(gx * KV), 512, 0, s>>>(out, q, kc, vc, ks, vs, tables, W, tseq,
                                                                            tkvl, T, H, KV, lg, sl2, order);
     } else {
-        paged_prefill_kernel<REP, SM, false><<<dim3(gx, KV), 256, 0, s>>>(out, q, kc, vc, ks, vs, tables, W, tseq,
+        paged_prefill_kernel<REP, SM, false><<<dim3(gx * KV), 256, 0, s>>>(out, q, kc, vc, ks, vs, tables, W, tseq,
                                                                            tkvl, T, H, KV, lg, sl2, nullptr);
     }
     return hipGetLastError() == hipSuccess ? CVH_OK : CVH_ERR_LAUNCH;
@@ -578,7 +581,7 @@ int prefill_entry(void* out, const void* q, const uint8_t* k_cache, const uint8_
     if (scale_mode != CVH_SCALE_PER_TOKEN_HEAD && scale_mode != CVH_SCALE_PER_TENSOR) return CVH_ERR_UNSUPPORTED;
     if (num_tokens > (int64_t{1} << 30)) return CVH_ERR_UNSUPPORTED;
     if (table_width > (int64_t{0x7fffffff} >> lg)) return CVH_ERR_UNSUPPORTED;    // contexts < 2^31 keys
-    if (order && (num_tokens + kWgTok - 1) / kWgTok * n_kv_heads > 0x7fffffff) return CVH_ERR_UNSUPPORTED;
+    if ((num_tokens + kWgTok - 1) / kWgTok * n_kv_heads > 0x7fffffff) return CVH_ERR_UNSUPPORTED;   // 1-D grid
     auto s = reinterpret_cast<hipStream_t>(stream);
     const float sl2 = static_cast<float>(scale) * kLog2eP;
     auto* o = static_cast<uint16_t*>(out);
