@@ -104,6 +104,7 @@ def run_e2e(args):
     eng.generate([[1, 2, 3, 4, 5, 6, 7, 8]], SamplingParams(max_tokens=16, ignore_eos=True))   # warm-up
     prompts, outs = e2e_requests(n=args.e2e_requests)
     before = eng.stats()
+    rep0, rows0, keys0 = eng.runner.decode_replays, eng.runner.decode_rows, eng.runner.decode_keys
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for p, n in zip(prompts, outs):
@@ -118,6 +119,12 @@ def run_e2e(args):
     total = sum(len(v) for v in got.values())
     assert total == sum(outs), (total, sum(outs))
     after = eng.stats()
+    run = eng.runner
+    c = eng.model.cfg
+    reps = max(run.decode_replays - rep0, 1)
+    # algorithmic bytes of one decode-attention launch (one layer), averaged over the graph replays
+    dec_bytes = ((run.decode_keys - keys0) * c.n_kv_heads * (2 * c.head_dim + 8)
+                 + 2 * (run.decode_rows - rows0) * c.n_heads * c.head_dim * 2) / reps
     return {
         "metric": "e2e output tok/s (config 5)", "value": round(total / dt, 2), "unit": "tok/s",
         "n_gpus": 1, "steps": steps, "warmup": 1, "ms_per_step": round(dt * 1e3 / max(steps, 1), 4),
@@ -128,7 +135,10 @@ def run_e2e(args):
                    "requests": len(prompts), "output_tokens": total, "prompt_tokens": sum(len(p) for p in prompts),
                    "seconds": round(dt, 3), "block_size": cfg.block_size, "kv_blocks": eng.num_blocks,
                    "preemptions": after.preemptions - before.preemptions, "init_s": round(init_s, 1),
-                   "launch": "eager" if args.eager else "hip_graph"},
+                   "launch": "eager" if args.eager else "hip_graph",
+                   "decode_replays": run.decode_replays - rep0,
+                   "decode_rows_avg": round((run.decode_rows - rows0) / reps, 1),
+                   "decode_attn_bytes_per_launch": round(dec_bytes)},
     }
 
 

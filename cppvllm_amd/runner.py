@@ -277,6 +277,10 @@ class ModelRunner:
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.graphs_shared: dict[int, torch.cuda.CUDAGraph] = {}
         self.shared_replays = 0
+        # decode graph replays and the keys their real rows attend over (for per-launch byte counts)
+        self.decode_replays = 0
+        self.decode_rows = 0
+        self.decode_keys = 0
         if not enforce_eager:
             self.capture_graphs()
         self.warm_sampler()
@@ -441,6 +445,9 @@ class ModelRunner:
                 fused.feed_tokens(self.g_tok[:n], self.g_feed[:n], self._prev_sampled())
             (self.graphs_shared if any_shared else self.graphs)[B].replay()
             self.shared_replays += int(any_shared)
+            self.decode_replays += 1
+            self.decode_rows += n
+            self.decode_keys += int(batch.positions[t0].sum()) + n
             self._sample(self.g_hidden[:n], out[d0:d1], temps_dev_g)
         if first_eager < S:
             a = first_eager
