@@ -217,3 +217,35 @@ def test_token_metadata_matches_oracle(orc):
     assert np.array_equal(seq.cpu().numpy(), ws)
     assert np.array_equal(slot.cpu().numpy(), wsl)
     assert np.array_equal(kvl.cpu().numpy(), wk)
+
+
+# (H, KV, HD) layouts, block sizes and row counts drawn per seed for the bit-exact sweep below
+_QKV_LAYOUTS = [(16, 8, 128), (8, 8, 128), (32, 8, 128), (64, 8, 128), (8, 2, 64), (2, 1, 128), (4, 4, 64),
+                (16, 4, 128)]
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_qk_norm_rope_kv_write_random_bitexact(orc, seed):
+    """Seeded random layouts, block sizes 16-1024, 1-600 rows with random positions and slots (some
+    -1), qkv magnitudes from 1e-3 to 30 (so the per-(token, head) scales span many binades), both
+    scale modes, with and without the dense K/V outputs: q, cache bytes and scales bit-exact."""
+    r = np.random.default_rng(seed)
+    H, KV, HD = _QKV_LAYOUTS[r.integers(len(_QKV_LAYOUTS))]
+    BS = int([16, 32, 64, 256, 1024][r.integers(5)])
+    T = int(r.integers(1, 601))
+    per_tensor, dense = bool(r.integers(2)), bool(r.integers(2))
+    mag = float(10.0 ** r.uniform(-3, 1.5))
+    say(f"qk_norm_rope_kv_write random seed={seed} H={H} KV={KV} HD={HD} BS={BS} T={T} per_tensor={per_tensor} "
+        f"dense={dense} mag={mag:.3g}")
+    g = torch.Generator().manual_seed(500 + seed)
+    nb = math.ceil(T / BS) + 2
+    w = {
+        "n_heads": H, "n_kv_heads": KV, "max_position": 8192,
+        "qkv": (torch.randn((T, (H + 2 * KV) * HD), generator=g) * mag).to(torch.bfloat16),
+        "q_norm": (torch.rand((HD,), generator=g) + 0.5).to(torch.bfloat16),
+        "k_norm": (torch.rand((HD,), generator=g) + 0.5).to(torch.bfloat16),
+        "positions": torch.randint(0, 8192, (T,), generator=g),
+        "slots": torch.randperm(nb * BS, generator=g)[:T],
+    }
+    w["slots"][torch.rand((T,), generator=g) < 0.1] = -1
+    _run_qkv(orc, w, HD, BS, per_tensor, dense, nb=nb)
