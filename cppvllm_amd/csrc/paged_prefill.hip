@@ -183,6 +183,12 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 
     f32x4_t o[REP][8];
     float m[REP], lsum[REP];
+    // Power-of-two range of the fp16 PV weights, wave-uniform: w = exp2(s - m - e) * vs with
+    // vs * 2^-e <= 2^7 for the largest V scale of the tile, so w <= 2^15 whatever the magnitude of
+    // V (per-(token, head) or per-tensor scales from 1e-11 to 1e38) and the tile's largest weights
+    // stay normal fp16 numbers. e acts as an offset of the running max: l and O carry the same
+    // 2^-e, a change of e rescales both like a move of the max, and O / l is unchanged.
+    float ew = 0.f;
 #pragma unroll
     for (int rb = 0; rb < REP; ++rb) {
         m[rb] = kNegHuge;
@@ -344,6 +350,18 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                 ksr[kb][0] = a.x; ksr[kb][1] = a.y; ksr[kb][2] = a.z; ksr[kb][3] = a.w;
                 vsr[kb][0] = b.x; vsr[kb][1] = b.y; vsr[kb][2] = b.z; vsr[kb][3] = b.w;
             }
+            // the tile's largest V scale (scales are >= 0; keys past a context read 0); a new
+            // range exponent only when it leaves [2^-6, 2^7) x 2^e
+            const float e_old = ew;
+            {
+                float vm = fmaxf(fmaxf(fmaxf(vsr[0][0], vsr[0][1]), fmaxf(vsr[0][2], vsr[0][3])),
+                                 fmaxf(fmaxf(vsr[1][0], vsr[1][1]), fmaxf(vsr[1][2], vsr[1][3])));
+                vm = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(max_groups(vm))));
+                const int vexp = ((__float_as_int(vm) >> 23) & 0xff) - 127;      // floor(log2 vm), vm normal
+                const float rel = static_cast<float>(vexp) - ew;
+                // (kept within [-100, 120]: p' = exp2(s - m - e) <= 2^108 stays a finite fp32)
+                if (vm > 0.f && (rel >= 7.f || rel < -6.f)) ew = static_cast<float>(min(max(vexp - 6, -100), 120));
+            }
 #pragma unroll
             for (int rb = 0; rb < REP; ++rb) {
 #pragma unroll
@@ -366,9 +384,10 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                 // the running max only moves when the tile's max exceeds it by more than 2^8 (a
                 // stale max leaves p <= 2^8: exact in fp32, the same relative bf16 rounding), so
                 // most tiles skip the rescale of O
-                const float mn = mt > m[rb] + kRescaleLog2 ? mt : m[rb];
-                const float alpha = __builtin_amdgcn_exp2f(m[rb] - mn);
-                m[rb] = mn;
+                const float mn0 = mt > m[rb] + kRescaleLog2 ? mt : m[rb];
+                const float alpha = __builtin_amdgcn_exp2f((m[rb] + e_old) - (mn0 + ew));
+                m[rb] = mn0;
+                const float mn = mn0 + ew;                                   // offset max of this tile's p
                 float ps = 0.f;
                 uint32_t pp[4];
 #pragma unroll
@@ -425,7 +444,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
             for (int rb = 0; rb < REP; ++rb) {
                 float* d = xs + rb * kVals * 256 + tid;
-                d[0] = m[rb];
+                d[0] = m[rb] + ew;                  // l and O of this half carry 2^-ew
                 d[256] = sum_groups(lsum[rb]);
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
@@ -439,9 +458,9 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
 #pragma unroll
         for (int rb = 0; rb < REP; ++rb) {
             const float* d = xs + rb * kVals * 256 + tid;
-            const float m1 = d[0], l1 = d[256];
-            const float mn = fmaxf(m[rb], m1);
-            const float a0 = __builtin_amdgcn_exp2f(m[rb] - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
+            const float m0 = m[rb] + ew, m1 = d[0], l1 = d[256];
+            const float mn = fmaxf(m0, m1);
+            const float a0 = __builtin_amdgcn_exp2f(m0 - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
             const float l = sum_groups(lsum[rb]) * a0 + l1 * a1;
             const float inv = l > 0.f ? 1.0f / l : 0.f;
             uint16_t* orow = out + (static_cast<int64_t>(tq) * H + kvh * REP + rb) * kHD;

@@ -1,0 +1,56 @@
+"""Attention outputs across V magnitudes, against the CPU oracle, through the C ABI.
+
+The V scales (per (token, head) or per tensor) are multiplied by a factor f from 1e-6 to 3e5: the
+codes stay the same, so V, and every output row, scale by exactly f in the oracle. Each entry
+point (decode on VALU at GQA 2, decode on MFMA at GQA 8, the multi-query kernel plain and
+planned) is checked on outputs divided by f at the build's bar (max-abs 2e-2, mean-abs 2e-3, one
+bf16 ulp allowed), so a format whose range or precision depends on the magnitude of V (an fp16
+product of softmax weight and V scale would overflow above ~1e5 and lose bits below ~1e-3) fails.
+"""
+import numpy as np
+import pytest
+
+from tests._util import bf16_vals, bf16_ulp, say
+from tests.test_gpu_attention import dev, run_gpu, run_oracle, run_planned, synth, synth_prefill
+
+pytestmark = pytest.mark.gpu
+
+FACTORS = [1e-6, 1e-3, 1.0, 1e3, 3e5]
+
+
+def _check_scaled(got_bits, want_bits, f):
+    g = bf16_vals(got_bits).astype(np.float64) / f
+    w = bf16_vals(want_bits).astype(np.float64) / f
+    assert np.isfinite(g).all(), "non-finite output"
+    err = np.abs(g - w)
+    tol = np.maximum(2e-2, bf16_ulp(w))
+    assert (err <= tol).all(), f"max-abs {err.max():.3e} (scaled by 1/{f:g})"
+    assert err.mean() <= 2e-3, f"mean-abs {err.mean():.3e} (scaled by 1/{f:g})"
+
+
+def _scale_v(b, f):
+    b = dict(b)
+    b["v_scale"] = b["v_scale"] * f
+    return b
+
+
+@pytest.mark.parametrize("f", FACTORS)
+@pytest.mark.parametrize("per_tensor", [False, True])
+@pytest.mark.parametrize("H", [16, 64])
+def test_decode_v_magnitudes(orc, f, per_tensor, H):
+    say(f"decode V magnitude f={f:g} per_tensor={per_tensor} H={H}")
+    b = _scale_v(synth(71, [40, 300, 1000, 17, 2500], 16, H=H, KV=8, per_tensor=per_tensor), f)
+    want = run_oracle(orc, b)
+    db = dev(b)
+    got = run_gpu(db)
+    _check_scaled(got, want, f)
+    assert np.array_equal(run_planned(db), got)
+
+
+@pytest.mark.parametrize("f", FACTORS)
+@pytest.mark.parametrize("per_tensor", [False, True])
+@pytest.mark.parametrize("mode", [True, "planned"])
+def test_prefill_v_magnitudes(orc, f, per_tensor, mode):
+    say(f"prefill V magnitude f={f:g} per_tensor={per_tensor} mode={mode}")
+    b = _scale_v(synth_prefill(72, [(300, 300), (1000, 70), (40, 40)], 16, per_tensor=per_tensor), f)
+    _check_scaled(run_gpu(dev(b), prefill=mode), run_oracle(orc, b), f)
