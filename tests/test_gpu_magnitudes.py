@@ -1,4 +1,5 @@
-"""Attention outputs across V magnitudes, against the CPU oracle, through the C ABI.
+"""Attention outputs across V and K magnitudes, and with kv_len beyond the block table, against
+the CPU oracle, through the C ABI.
 
 The V scales (per (token, head) or per tensor) are multiplied by a factor f from 1e-6 to 3e5: the
 codes stay the same, so V, and every output row, scale by exactly f in the oracle. Each entry
@@ -9,6 +10,7 @@ product of softmax weight and V scale would overflow above ~1e5 and lose bits be
 """
 import numpy as np
 import pytest
+import torch
 
 from tests._util import bf16_vals, bf16_ulp, say
 from tests.test_gpu_attention import dev, run_gpu, run_oracle, run_planned, synth, synth_prefill
@@ -78,3 +80,22 @@ def test_k_magnitudes_all_paths(orc, fk, per_tensor):
     want = run_oracle(orc, b)
     for mode in (True, "planned"):
         _check_scaled(run_gpu(dev(b), prefill=mode), want, 1e3)
+
+
+@pytest.mark.parametrize("BS", [16, 256])
+def test_kv_len_beyond_table_is_clamped(orc, BS):
+    """token_kv_len larger than a row's block table holds (table_width x block_size) attends over the
+    whole table, in every entry point as in the oracle (cvh_oracle.c clamps L the same way)."""
+    say(f"kv_len beyond the table BS={BS}")
+    b = synth(75, [40, 300, 1000, 17, 700], BS, queries_per_seq=3)
+    W = b["block_tables"].shape[1]
+    longest = int(np.argmax([40, 300, 1000, 17, 700]))
+    rows = (b["token_seq"] == longest).nonzero().flatten()
+    b["token_kv_len"][rows] = W * BS + 100 + torch.arange(rows.numel())
+    want = run_oracle(orc, b)
+    db = dev(b)
+    got = run_gpu(db)
+    _check_scaled(got, want, 1.0)
+    assert np.array_equal(run_planned(db), got)
+    for mode in (True, "planned"):
+        _check_scaled(run_gpu(db, prefill=mode), want, 1.0)
