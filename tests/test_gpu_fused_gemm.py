@@ -238,3 +238,60 @@ def test_residual_then_rownorm_matches_add_rms_norm_path(M):
     say(f"  vs exact: fused max {e_fused.max():.3e} mean {e_fused.mean():.3e}; "
         f"unfused max {e_unfused.max():.3e} mean {e_unfused.mean():.3e}")
     assert e_fused.max() <= 1.25 * e_unfused.max() and e_fused.mean() <= 1.25 * e_unfused.mean()
+
+
+def _special_rows(g, M, D):
+    """Residual rows whose sum of squares is zero, underflows (1e-25), is large but finite (1e15)
+    or overflows to inf (1e19), among ordinary rows."""
+    v = rnd(g, M, D).float()
+    v[0] = 0.0
+    v[1] *= 1e-25
+    v[2] *= 1e15
+    v[3] *= 1e19
+    return v.to(torch.bfloat16)
+
+
+def test_residual_epilogue_special_rows_bitexact():
+    """The residual add and its partial sums of squares on rows of extreme magnitude (sums of
+    squares that underflow to 0 or overflow to inf), bit for bit against the restatement."""
+    M, N, K = 16, 1024, 2048
+    g = torch.Generator().manual_seed(91)
+    x, w, r0 = rnd(g, M, K), rnd(g, N, K, std=0.02), _special_rows(g, M, N)
+    x[:2] = 0                    # rows 0, 1: the projection adds exact zeros, so the sums stay 0 / tiny
+    xd, wd = x.to(DEV), w.to(DEV)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    ops.linear(y, xd, wd, TILED_PLAIN)
+    want = (r0.to(DEV).float() + y.float()).to(torch.bfloat16)
+    want_ss = ss_restated(bits(want))
+    assert np.isinf(want_ss[3]).any() and (want_ss[0] == 0).all() and (want_ss[1] == 0).all()
+    for c in codes(ops.FUSED_RESIDUAL) + [0]:
+        say(f"residual epilogue special rows config={c}")
+        resid = r0.to(DEV)
+        ss = torch.full((M, N // 16), float("nan"), device=DEV)
+        ops.linear_residual(resid, ss, xd, wd, c)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(resid), bits(want)), f"config {c}"
+        assert np.array_equal(f32_bits(ss), want_ss.view(np.uint32)), f"config {c}"
+
+
+def test_swiglu_rownorm_special_rows():
+    """Row-normed gate/up on those rows: the row factor from the partials is 1/sqrt(eps) for a zero
+    or underflowing sum and 0 for an overflowing one, as in the float64 restatement; outputs are
+    finite and within the bar."""
+    M, D, I, eps = 16, 1024, 3072, 1e-6
+    g = torch.Generator().manual_seed(92)
+    v = _special_rows(g, M, D)
+    gain = (torch.rand((D,), generator=g) + 0.5).to(torch.bfloat16)
+    wf = ops.fold_norm_gain(ops.interleave_gate_up(rnd(g, 2 * I, D, std=0.02)), gain)
+    ss = torch.from_numpy(ss_restated(bits(v)))
+    gu = _rownorm_ref(v, ss, wf, eps).to(torch.bfloat16).view(M, I // 16, 2, 16)
+    gate, up = gu[:, :, 0, :].reshape(M, I), gu[:, :, 1, :].reshape(M, I)
+    act_want = torch.empty((M, I), dtype=torch.bfloat16, device=DEV)
+    ops.fused.swiglu(act_want, torch.cat([gate, up], 1).to(DEV))
+    for c in codes(ops.FUSED_SWIGLU_ROWNORM) + [0]:
+        say(f"swiglu rownorm special rows config={c}")
+        act = torch.empty((M, I), dtype=torch.bfloat16, device=DEV)
+        ops.linear_swiglu_rownorm(act, v.to(DEV), ss.to(DEV), eps, wf.to(DEV), c)
+        torch.cuda.synchronize()
+        assert torch.isfinite(act.float()).all(), f"config {c}"
+        _bar(act, act_want, f"config {c}")
