@@ -41,10 +41,11 @@ def ss_restated(v_bits: np.ndarray) -> np.ndarray:
     M, N = v.shape
     q = v.reshape(M, N // 16, 4, 4)
     s = np.zeros((M, N // 16, 4), np.float32)
-    for r in range(4):
-        s = (s + q[..., r] * q[..., r]).astype(np.float32)
-    return ((s[..., 0] + s[..., 1]).astype(np.float32) + (s[..., 2] + s[..., 3]).astype(np.float32)).astype(
-        np.float32)
+    with np.errstate(over="ignore"):               # rows of huge values overflow to inf, as on the GPU
+        for r in range(4):
+            s = (s + q[..., r] * q[..., r]).astype(np.float32)
+        return ((s[..., 0] + s[..., 1]).astype(np.float32) + (s[..., 2] + s[..., 3]).astype(np.float32)).astype(
+            np.float32)
 
 
 def inv_restated(ss: np.ndarray, K: int, eps: float) -> np.ndarray:
