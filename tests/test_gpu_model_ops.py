@@ -87,6 +87,29 @@ def test_sampler_rows_and_temperatures(orc):
         assert np.array_equal(got, want), f"V={V}: got {got} want {want}"
 
 
+def test_sampler_extreme_temperatures_and_logits(orc):
+    """Gumbel rows at temperatures 1e-30 (x / t overflows to +-inf), 1e30 (the noise decides) and
+    1, on logits with +-inf, NaN and 1e38 entries, against the oracle: same token."""
+    say("gumbel sampler extreme temperatures / logits V=151936")
+    g = torch.Generator().manual_seed(14)
+    R, V = 9, 151936
+    lg = torch.randn((R, V), generator=g)
+    for base in (0, 3, 6):
+        lg[base + 1, 100] = float("inf")
+        lg[base + 1, 200] = float("-inf")
+        lg[base + 2, 50:60] = float("nan")
+        lg[base + 2, 70000] = 3e38
+        lg[base + 2, 70001] = -3e38
+    temps = torch.tensor([1e-30, 1e-30, 1e-30, 1e30, 1e30, 1e30, 1.0, 1.0, 1.0], dtype=torch.float32)
+    out = torch.empty(R, dtype=torch.int64, device=DEV)
+    for seed, off in ((1, 0), (0xDEADBEEF12345678, 7)):
+        ops.fused.sample_tokens(out, lg.to(DEV), None, temps.to(DEV), seed, off)
+        torch.cuda.synchronize()
+        want = orc.sample_tokens(lg.numpy(), temps=temps.numpy(), seed=seed, offset=off)
+        got = out.cpu().numpy()
+        assert np.array_equal(got, want), f"seed {seed}: got {got} want {want}"
+
+
 def test_feed_tokens_and_embedding():
     say("feed_tokens / embedding")
     prev = torch.tensor([100, 101, 102, 103], dtype=torch.int64, device=DEV)
