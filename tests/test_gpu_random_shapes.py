@@ -1,6 +1,6 @@
 """Seeded random sweep of the attention entry points against the CPU oracle, through the C ABI.
 
-Each case draws a head layout, block size, scale mode, partition count and a ragged batch (1-40
+Each case draws a head layout, block size (16-4096), scale mode, partition count and a ragged batch (1-40
 sequences, contexts log-uniform in [1, 3000] keys, 1-3 trailing query tokens per sequence; or
 100-300 sequences of one token with contexts up to 6000 keys), with a few empty or padding rows,
 and checks: the plain decode launch against the oracle at the build's bar (max-abs 2e-2, mean-abs
@@ -30,7 +30,8 @@ def draw(seed, wide=False):
     """wide: a decode-sized batch (100-300 sequences, one query token each, contexts up to 6000)."""
     r = np.random.default_rng(seed)
     H, KV, HD = LAYOUTS[r.integers(len(LAYOUTS))]
-    BS = int(BLOCK_SIZES[r.integers(len(BLOCK_SIZES))])
+    sizes = BLOCK_SIZES if wide else BLOCK_SIZES + [2048, 4096]    # (wide batches: host memory)
+    BS = int(sizes[r.integers(len(sizes))])
     n = int(r.integers(100, 301)) if wide else int(r.integers(1, 41))
     lens = [max(1, int(math.exp(r.uniform(0, math.log(6000 if wide else 3000))))) for _ in range(n)]
     qps = 1 if wide else int(r.integers(1, 4))
