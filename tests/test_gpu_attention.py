@@ -328,6 +328,44 @@ def test_graph_replay_matches_eager():
         _ = run_gpu(b)   # eager work between replays
 
 
+def test_prefill_plan_and_kernel_graph_replay():
+    """The prefill plan and the planned multi-query launch captured in one HIP graph (as the engine
+    runs prompt steps): every replay, with new q, token lengths and eager work in between, equals
+    the eager launch on the same inputs."""
+    say("prefill plan + planned kernel: graph capture + 3 replays")
+    b = dev(synth_prefill(44, [(300, 300), (1000, 70), (40, 40), (700, 129)], 16))
+    T = b["q"].shape[0]
+    pws = ops.prefill_workspace(T, DEV)
+    out = torch.empty_like(b["q"])
+
+    def body():
+        ops.paged_attention_prefill_plan(b["token_seq"], b["token_kv_len"], b["block_tables"].shape[1],
+                                         b["block_size"], pws)
+        ops.paged_attention_fp8_prefill(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
+                                        b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"],
+                                        workspace=pws)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):   # warm-up on the capture stream
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        body()
+    gen = torch.Generator().manual_seed(45)
+    kvl0 = b["token_kv_len"].clone()
+    for i in range(3):
+        b["q"].copy_(torch.randn(b["q"].shape, generator=gen).to(torch.bfloat16))
+        b["token_kv_len"].copy_((kvl0 - i * 7).clamp_min(0))     # new lengths: the plan must follow them
+        eager = run_gpu(b, prefill="planned")
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), eager), f"replay {i} differs from eager"
+
+
 def test_split_and_merge_phases_equal_combined_call():
     say("split phase + merge phase == combined call")
     from cppvllm_amd import _lib
