@@ -189,6 +189,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     // stay normal fp16 numbers. e acts as an offset of the running max: l and O carry the same
     // 2^-e, a change of e rescales both like a move of the max, and O / l is unchanged.
     float ew = 0.f;
+    float win_hi = 128.f, win_lo = 1.0f / 64.f;     // [2^(e-6), 2^(e+7)): the tile max needs no new e
 #pragma unroll
     for (int rb = 0; rb < REP; ++rb) {
         m[rb] = kNegHuge;
@@ -352,15 +353,25 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
             }
             // the tile's largest V scale (scales are >= 0; keys past a context read 0); a new
             // range exponent only when it leaves [2^-6, 2^7) x 2^e
+            // (each lane tests its own 8 keys; only when some lane is above the window, or none
+            // reaches it, does the wave reduce the maximum and move e, kept within [-100, 120] so
+            // that p' = exp2(s - m - e) <= 2^108 stays a finite fp32)
             const float e_old = ew;
             {
                 float vm = fmaxf(fmaxf(fmaxf(vsr[0][0], vsr[0][1]), fmaxf(vsr[0][2], vsr[0][3])),
                                  fmaxf(fmaxf(vsr[1][0], vsr[1][1]), fmaxf(vsr[1][2], vsr[1][3])));
-                vm = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(max_groups(vm))));
-                const int vexp = ((__float_as_int(vm) >> 23) & 0xff) - 127;      // floor(log2 vm), vm normal
-                const float rel = static_cast<float>(vexp) - ew;
-                // (kept within [-100, 120]: p' = exp2(s - m - e) <= 2^108 stays a finite fp32)
-                if (vm > 0.f && (rel >= 7.f || rel < -6.f)) ew = static_cast<float>(min(max(vexp - 6, -100), 120));
+                const uint64_t above = __builtin_amdgcn_ballot_w64(vm >= win_hi);
+                const uint64_t inside = __builtin_amdgcn_ballot_w64(vm >= win_lo);
+                if (above != 0 || inside == 0) {
+                    vm = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(max_groups(vm))));
+                    if (vm > 0.f) {
+                        const int vexp = ((__float_as_int(vm) >> 23) & 0xff) - 127;   // floor(log2 vm), vm normal
+                        const int en = min(max(vexp - 6, -100), 120);
+                        ew = static_cast<float>(en);
+                        win_hi = __builtin_ldexpf(1.0f, en + 7);
+                        win_lo = __builtin_ldexpf(1.0f, en - 6);
+                    }
+                }
             }
 #pragma unroll
             for (int rb = 0; rb < REP; ++rb) {
