@@ -64,19 +64,22 @@ def cpu_baseline(b, reps: int = 5):
     args = [host(b[k]) for k in ("q", "k_cache", "v_cache", "k_scale", "v_scale", "block_tables", "token_seq",
                                  "token_kv_len")]
     H, KV, HD, BS = b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
+    # one warm-up layer, then at least `reps` layers and about 10 s of timed CPU work
     times = []
-    for i in range(reps + 1):
+    i = 0
+    while i <= reps or sum(times) < 10.0:
         t0 = time.perf_counter()
         oracle.paged_attention_fp8(*args, H, KV, HD, BS, oracle.PER_TOKEN_HEAD, b["scale"])
         if i:
             times.append(time.perf_counter() - t0)
+        i += 1
     med = statistics.median(times)
     nbytes = workloads.attention_bytes(args[7].tolist(), n_kv=KV, n_heads=H)
     return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
             "omp_max_threads": oracle.max_threads(),
             "sample": f"one layer of config 3 (all 256 tokens, {nbytes / 1e6:.1f} MB algorithmic), "
-                      f"median of {reps} after 1 warm-up: {med * 1e3:.1f} ms/layer"}
+                      f"median of {len(times)} ({sum(times):.1f} s timed) after 1 warm-up: {med * 1e3:.1f} ms/layer"}
 
 
 def e2e_requests(seed: int = 1005, n: int = 256):
