@@ -81,4 +81,4 @@ extern "C" int cvh_rope_tables_host(float* cos_t, float* sin_t, int64_t max_posi
     return CVH_OK;
 }
 
-extern "C" const char* cvh_version(void) { return "cppvllm-mi355x 0.1 (gfx950)"; }
+extern "C" const char* cvh_version(void) { return "cppvllm-mi355x 0.2 (gfx950)"; }

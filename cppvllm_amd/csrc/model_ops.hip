@@ -108,7 +108,8 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32
 }
 
 __device__ __forceinline__ uint64_t rank_key(float s, uint32_t index) {
-    const uint32_t b = __float_as_uint(s);
+    uint32_t b = __float_as_uint(s);
+    if (b == 0x80000000u) b = 0u;                  // -0.0 ties with +0.0 (lower index wins)
     uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     if ((b & 0x7fffffffu) > 0x7f800000u) o = 0u;   // NaN: below -inf
     return (static_cast<uint64_t>(o) << 32) | (0xFFFFFFFFu - index);

@@ -1589,11 +1589,12 @@ extern "C" int cvh_paged_attention_fp8(void* out, const void* q, const uint8_t* 
 // one GPU (two streams, or two host threads) share the array and race.
 namespace cvh {
 namespace {
-// 8 MiB. With automatic partitions every supported launch fits: partials are at most
-// G * 2 * (heads per row group) <= (2048 / wpg) * 2 * (2 * wpg) = 8192 slots of HD floats (4 MiB at
-// HD 128), plus the prefix, token and plan records of at most 8192 rows (< 0.5 MiB). Explicit
-// partition counts beyond that are rejected.
-constexpr size_t kScratchBytes = size_t{8} << 20;
+// 24 MiB. With automatic partitions every supported launch fits: partials are at most
+// G * 2 * (heads per row group) = G * 2 * wpg * REP <= 2048 * 2 * 8 = 32768 slots of HD floats
+// (16 MiB at HD 128, GQA 8; G * wpg never exceeds the 2048 resident waves), plus their (max, sum)
+// pairs (256 KiB) and the prefix, token and plan records of at most 8192 rows (< 0.5 MiB).
+// Explicit partition counts beyond that are rejected.
+constexpr size_t kScratchBytes = size_t{24} << 20;
 constexpr int kMaxDevices = 64;
 }  // namespace
 }  // namespace cvh

@@ -40,6 +40,9 @@ class EngineConfig:
     seed: int = 0
     weight_std: float = 0.02
     eos_token_id: int = 151645
+    # True: every step rounds at the reference's points (add_rms_norm output rounded to bf16 before
+    # each projection); False: decode batches of 16-256 rows use the fused-epilogue projections
+    exact_norm_rounding: bool = False
     extra: dict = field(default_factory=dict)
 
 
@@ -49,6 +52,7 @@ class LLMEngine:
         self.model_cfg = mc = model_cfg or Qwen3Config()
         self.device = torch.device(device)
         self.model = Qwen3(mc, self.device, seed=cfg.seed, std=cfg.weight_std)
+        self.model.fused_epilogues = not cfg.exact_norm_rounding
         self.num_blocks = self._size_kv_cache()
         self.cache = KVCache(mc, self.num_blocks, cfg.block_size, self.device)
         self.runner = ModelRunner(self.model, self.cache, max_num_batched_tokens=cfg.max_num_batched_tokens,

@@ -121,6 +121,10 @@ class Qwen3:
         self.cos, self.sin = cos.to(device), sin.to(device)
         self.scale = 1.0 / math.sqrt(HD)
         self.unit_gain = ones(D)
+        # False: every batch uses the reference's rounding points (normed input rounded to bf16, then
+        # the gain, then the projection); True: batches of FUSED_MIN_ROWS..GEMM_MAX_ROWS rows take the
+        # fused-epilogue projections, which round the gain-scaled weights instead
+        self.fused_epilogues = True
         self.fold_gains()
 
     def fold_gains(self) -> None:
@@ -128,7 +132,9 @@ class Qwen3:
         the projections they feed (ops.fold_norm_gain; the same tensor where the gain is all ones).
         Call again after changing attn_norm / ffn_norm."""
         c = self.cfg
-        self.fused_ok = (c.head_dim == 128 and c.dim % 256 == 0 and c.dim <= 1024 and self.gate_up_interleaved)
+        # the gate/up row-normed tile above 128 rows is 128 columns wide, so 2I must be a multiple of 128
+        self.fused_ok = (c.head_dim == 128 and c.dim % 256 == 0 and c.dim <= 1024 and self.gate_up_interleaved
+                         and (2 * c.intermediate_size) % 128 == 0)
         fold = lambda w, gain: w if bool((gain == 1).all()) else ops.fold_norm_gain(w, gain)  # noqa: E731
         self.wqkv_f = [fold(w, g) for w, g in zip(self.wqkv, self.attn_norm)]
         self.w_gu_f = [fold(w, g) for w, g in zip(self.w_gu, self.ffn_norm)] if self.fused_ok else []
@@ -169,7 +175,7 @@ class Qwen3:
                 ops.paged_attention_fp8(att, q, kc, vc, ks, vs, block_tables, seq, kvl, self.scale,
                                         workspace=workspace, planned=planned, shared=shared)
 
-        if self.fused_ok and FUSED_MIN_ROWS <= T <= GEMM_MAX_ROWS:
+        if self.fused_ok and self.fused_epilogues and FUSED_MIN_ROWS <= T <= GEMM_MAX_ROWS:
             # Layer boundaries in the projections' epilogues: o_proj / down_proj add into the
             # residual h and leave its per-16-column sums of squares in ss; qkv / gate-up take h
             # raw and apply the row's RMS factor from ss (gains folded into their weights); qkv
@@ -281,6 +287,13 @@ class ModelRunner:
         self.decode_replays = 0
         self.decode_rows = 0
         self.decode_keys = 0
+        # decode rows run the same forward with or without graphs: padded to a batch size of
+        # _graph_sizes, planned attention over the graph workspace (so a replay and an eager run of a
+        # decode step give the same bits)
+        self.graph_sizes = _graph_sizes(self.max_graph_batch)
+        Bmax = self.graph_sizes[-1]
+        self.ws_graph = ops.paged_attention_workspace(Bmax, c.n_heads, c.n_kv_heads, c.head_dim, Wg, BS, 0, dev)
+        self.g_hidden = torch.empty((Bmax, c.dim), dtype=torch.bfloat16, device=dev)
         if not enforce_eager:
             self.capture_graphs()
         self.warm_sampler()
@@ -331,12 +344,8 @@ class ModelRunner:
         self.g_hidden[:B].copy_(x)
 
     def capture_graphs(self) -> None:
-        c = self.model.cfg
-        sizes = _graph_sizes(self.max_graph_batch)
+        sizes = self.graph_sizes
         Bmax = sizes[-1]
-        self.ws_graph = ops.paged_attention_workspace(Bmax, c.n_heads, c.n_kv_heads, c.head_dim, self.graph_width,
-                                                      self.cache.block_size, 0, self.model.device)
-        self.g_hidden = torch.empty((Bmax, c.dim), dtype=torch.bfloat16, device=self.model.device)
         empty = np.zeros((0, self.graph_width), dtype=np.int64)
         self._stage_graph_rows([], [], empty, Bmax)
         torch.cuda.synchronize()
@@ -417,7 +426,7 @@ class ModelRunner:
         d0, d1 = batch.group_start[0], batch.group_start[1]
         cu = batch.cu_seqlens
         feed = batch.feed_src
-        use_graph = bool(self.graphs) and d1 > d0
+        use_graph = d1 > d0      # decode rows: a captured graph, or the same body run eagerly
         first_eager = d1 if use_graph else d0
         samp = np.nonzero(batch.samples[first_eager:])[0]
         # temperatures of the sampled rows: graph rows first, then the eager rows, one copy
@@ -435,7 +444,7 @@ class ModelRunner:
         if use_graph:
             t0 = cu[d0:d1]
             n = d1 - d0
-            B = next(b for b in sorted(self.graphs) if b >= n)
+            B = next(b for b in self.graph_sizes if b >= n)
             shared = None if batch.shared_blocks is None else batch.shared_blocks[d0:d1]
             any_shared = shared is not None and bool((shared > 0).any())
             need_feed = self._stage_graph_rows(batch.tokens[t0], batch.positions[t0], batch.block_tables[d0:d1], B,
@@ -443,7 +452,11 @@ class ModelRunner:
                                                shared if any_shared else None)
             if need_feed:
                 fused.feed_tokens(self.g_tok[:n], self.g_feed[:n], self._prev_sampled())
-            (self.graphs_shared if any_shared else self.graphs)[B].replay()
+            graphs = self.graphs_shared if any_shared else self.graphs
+            if graphs:
+                graphs[B].replay()
+            else:
+                self._graph_body(B, self.ws_graph, any_shared)
             self.shared_replays += int(any_shared)
             self.decode_replays += 1
             self.decode_rows += n

@@ -201,7 +201,7 @@ int cvh_paged_attention_fp8_planned_split_phase(void* out, const void* q, const 
                                                 int block_size, int scale_mode, double scale, int partitions,
                                                 void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 
-/* cvh_paged_attention_fp8_ex without a workspace argument: the split workspace is a fixed 8 MiB
+/* cvh_paged_attention_fp8_ex without a workspace argument: the split workspace is a fixed 24 MiB
  * device array inside the library (one per GPU, held until the process ends), so the call allocates
  * nothing and needs no caller buffer. No counterpart in the reference; it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid

@@ -187,7 +187,7 @@ def test_fused_path_with_norm_gains_matches_torch_reference():
                                       torch.arange(lens[j] + 1, device=DEV))[-1] for j in range(20)])
     errs = {}
     for fused_path in (False, True):
-        m.fused_ok = fused_path
+        m.fused_epilogues = fused_path     # False: the reference's rounding points (EngineConfig.exact_norm_rounding)
         say(f"  {'fused' if fused_path else 'unfused'}: prefill of 20 sequences ({b.num_tokens} rows), "
             "then a 20-row decode step")
         ep = (run(b) - want_p).abs()
@@ -228,6 +228,20 @@ def test_graph_decode_equals_eager_decode():
     assert torch.equal(k_after_graph[:, :nb], eng.cache.k[:, :nb])
     err = (xg - xe).abs()
     assert err.max().item() < 0.1 and err.mean().item() < 5e-3, (err.max().item(), err.mean().item())
+
+
+def test_eager_engine_equals_graph_engine():
+    """enforce_eager runs each decode step through the graph body without capturing it (same
+    padding rows, planned attention, partitions and GEMM tilings), so an eager engine and a graph
+    engine return the same tokens, including batches that cross graph sizes (1..8 rows)."""
+    say("engine: enforce_eager vs HIP graphs, 7 requests, exact tokens")
+    g = torch.Generator().manual_seed(26)
+    prompts = [torch.randint(0, SMALL.vocab_size, (n,), generator=g).tolist() for n in (5, 70, 33, 140, 9, 18, 2)]
+    params = [SamplingParams(max_tokens=n, ignore_eos=True) for n in (20, 3, 17, 9, 25, 40, 11)]
+    outs = [_engine(enforce_eager=eager, max_num_seqs=8, blocks=96).generate(prompts, params)
+            for eager in (True, False)]
+    assert outs[0] == outs[1]
+    assert [len(o) for o in outs[0]] == [20, 3, 17, 9, 25, 40, 11]
 
 
 def test_generate_greedy_with_chunked_prefill_and_graphs():

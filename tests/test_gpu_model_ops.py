@@ -60,6 +60,10 @@ def test_greedy_sampler_full_vocab(orc, ldtype):
     lg[9, :] = float("nan")
     lg[9, 70000] = float("-inf")                  # -inf beats NaN
     lg[10, :] = 1.0                               # all equal: index 0
+    lg[11, :] = -1.0
+    lg[11, 300], lg[11, 9000] = -0.0, 0.0         # signed zeros tie: the lower index (-0.0) wins
+    lg[12, :] = -1.0
+    lg[12, 300], lg[12, 9000] = 0.0, -0.0
     out = torch.empty(R, dtype=torch.int64, device=DEV)
     ops.fused.sample_tokens(out, lg.to(DEV), None, None, 0, 0)
     torch.cuda.synchronize()
@@ -69,6 +73,8 @@ def test_greedy_sampler_full_vocab(orc, ldtype):
     assert bad.size == 0, f"rows {bad[:8]}: got {got[bad[:8]]} want {want[bad[:8]]}"
     assert want[3] == 17 and want[4] == V - 1 and want[5] == 0 and want[6] == 0
     assert want[8] == 0x7FFFFFFF and want[9] == 70000 and want[10] == 0
+    assert want[11] == 300 and want[12] == 300
+    assert torch.signbit(lg[11, 300]) and not torch.signbit(lg[11, 9000])
 
 
 def test_sampler_rows_and_temperatures(orc):

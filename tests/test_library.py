@@ -227,3 +227,24 @@ def test_attention_byte_accounting():
     # 1 token, kv_len 10, KV=8, HD=128: 10*8*(256+8) + 2*16*128*2
     assert workloads.attention_bytes([10]) == 10 * 8 * 264 + 2 * 16 * 128 * 2
     assert workloads.attention_bytes([10], per_tensor=True) == 10 * 8 * 256 + 2 * 16 * 128 * 2
+
+
+def test_noalloc_array_holds_every_automatic_workspace():
+    """cvh_paged_attention_fp8_noalloc accepts every launch with automatic partitions: the
+    workspace of each supported head layout (GQA 1-8, head_dim 64/128, 1-64 kv heads), at every
+    token count up to the 8192-row limit, fits the fixed array."""
+    lib = _lib.lib()
+    mx = lib.cvh_paged_attention_noalloc_max_workspace()
+    worst = 0
+    for hd in (64, 128):
+        for kv in (1, 2, 3, 4, 8, 16, 32, 64):
+            for rep in (1, 2, 4, 8):
+                nkv = kv * (rep // 2 if (rep > 2 and hd != 128) else 1)   # the kernel's (virtual) kv heads
+                wpg = 8 if nkv % 8 == 0 else 4 if nkv % 4 == 0 else 2 if nkv % 2 == 0 else 1
+                tmax = 8192 // (nkv // wpg)                               # rows = T x row groups <= 8192
+                for T in sorted({1, 7, 64, 256, 1000, max(1, tmax)}):
+                    for W, bs in ((1, 16), (8, 256), (160, 256), (4096, 16)):
+                        n = lib.cvh_paged_attention_workspace_bytes(T, kv * rep, kv, hd, W, bs, 0)
+                        assert 0 < n <= mx, (hd, kv, rep, T, W, bs, n)
+                        worst = max(worst, n)
+    assert worst > mx // 2     # the bound is tight to within a factor of two (GQA 8: ~16.5 MiB)

@@ -77,10 +77,27 @@ def test_noalloc_equals_workspace_call_twice(orc):
     assert_close_bf16(got_small[rows], want)
 
 
+@pytest.mark.parametrize("H", [32, 64])
+def test_noalloc_gqa_mfma_twice(H):
+    """GQA 4 / 8 (the MFMA decode path, the largest automatic workspaces) at config-3 size, then
+    a smaller batch: bit for bit the workspace call."""
+    say(f"no-alloc attention: GQA {H // 8} config 3 then 24 seqs")
+    fn, mx = _noalloc()
+    for seqs, seed in ((256, 1003), (24, 1017)):
+        b = workloads.config3(device="cpu", seqs=seqs, seed=seed)
+        g = torch.Generator().manual_seed(H + seqs)
+        b["n_heads"] = H
+        b["q"] = torch.randn((seqs, H, 128), generator=g).to(torch.bfloat16)
+        b = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in b.items()}
+        n = _lib.lib().cvh_paged_attention_workspace_bytes(seqs, H, 8, 128, b["block_tables"].shape[1], 256, 0)
+        assert 0 < n <= mx()
+        assert np.array_equal(run_noalloc(b), run_with_workspace(b))
+
+
 def test_noalloc_rejects_oversize_and_bad_args():
     say("no-alloc attention: size limit and argument checks (nothing launched)")
     fn, mx = _noalloc()
-    assert mx() == 8 << 20
+    assert mx() == 24 << 20
     lib = _lib.lib()
     T, H, KV, HD, W, BS = 256, 16, 8, 128, 8, 256
     assert lib.cvh_paged_attention_workspace_bytes(T, H, KV, HD, W, BS, 0) <= mx()
