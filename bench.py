@@ -611,7 +611,9 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "paged_decode_kernel (%s split phase; graph of 28 back-to-back launches)"
                                % ("planned" if planned else "unplanned"),
-                     "avg_launch_us": round(avg_layer_ms * 1e3, 2)},
+                     "avg_launch_us": round(avg_layer_ms * 1e3, 2),
+                     "timing": "achieved = bytes_per_layer / avg_launch_us; avg_launch_us = HIP events around "
+                               "K replays of a graph of the 28 decode-kernel launches on the launch stream, / (28 K)"},
     }
     if not args.no_cpu:
         print("bench: CPU baseline (oracle, one layer)", flush=True, file=sys.stderr)
