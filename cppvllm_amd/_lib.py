@@ -13,6 +13,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libcppvllm_hip.so"
 HEADER = PKG.parent / "include" / "cppvllm_hip.h"
+RUNNER_HEADER = PKG.parent / "include" / "cppvllm_runner.h"
 
 CVH_OK = 0
 CVH_ERR_INVALID_ARG = 1
@@ -83,7 +84,31 @@ SIGNATURES = {
     "cvh_gemm_fused_configs": (i32, [i32, vp, i32]),
     "cvh_gemm_fused_config": (i32, [i32, i64]),
     "cvh_version": (C.c_char_p, []),
+    # include/cppvllm_runner.h
+    "cvh_runner_create": (i32, [vp, vp]),
+    "cvh_runner_destroy": (i32, [vp]),
+    "cvh_runner_stage": (i32, [vp, i32, i64, i32, vp, vp, vp, i64, vp, vp, vp, vp]),
+    "cvh_runner_forward": (i32, [vp, i32, i32, vp]),
+    "cvh_runner_capture": (i32, [vp, i32, i32]),
+    "cvh_runner_replay": (i32, [vp, i32, i32, vp]),
 }
+
+
+class RunnerLayer(C.Structure):
+    """struct cvh_runner_layer (include/cppvllm_runner.h)."""
+    _fields_ = [(n, vp) for n in ("w_qkv", "w_qkv_folded", "w_o", "w_gate_up", "w_gate_up_folded", "w_down",
+                                  "attn_norm", "ffn_norm", "q_norm", "k_norm", "k_cache", "v_cache", "k_scale",
+                                  "v_scale")]
+
+
+class RunnerDesc(C.Structure):
+    """struct cvh_runner_desc (include/cppvllm_runner.h)."""
+    _fields_ = [("n_layers", i32), ("dim", i32), ("n_heads", i32), ("n_kv_heads", i32), ("head_dim", i32),
+                ("intermediate", i32), ("vocab", i64), ("norm_eps", f64), ("attn_scale", f64), ("block_size", i32),
+                ("scale_mode", i32), ("max_batch", i32), ("table_width", i64), ("scratch_block", i64),
+                ("fused_min_rows", i32), ("fused_max_rows", i32), ("embed", vp), ("final_norm", vp),
+                ("unit_gain", vp), ("rope_cos", vp), ("rope_sin", vp), ("hidden", vp),
+                ("layers", C.POINTER(RunnerLayer))]
 
 _LIB = None
 
@@ -98,7 +123,7 @@ class CvhError(RuntimeError):
 
 def header_symbols() -> list[str]:
     """Function names declared in include/cppvllm_hip.h."""
-    text = HEADER.read_text()
+    text = HEADER.read_text() + RUNNER_HEADER.read_text()
     return sorted(set(re.findall(r"\b(cvh_[a-z0-9_]+)\s*\(", text)))
 
 

@@ -36,6 +36,7 @@ SOURCES = {
     "gemm.hip": ["-ffp-contract=off"],
     "batch_metadata.hip": ["-ffp-contract=off"],
     "model_ops.hip": ["-ffp-contract=off"],
+    "decode_runner.cpp": [],
 }
 
 

@@ -12,14 +12,17 @@ Mirrors the reference's runner/model split:
   * ``KVCache``            — ModelRunner::bind_cache layout (engine/model_runner.cpp:104-113):
                              K/V uint8 [L][NB+1][BS][KV][HD], scales f32 [L][NB+1][KV][BS]; block NB
                              is the scratch block that idle graph rows write to (:69,:346).
-  * ``ModelRunner.run``    — ModelRunner::launch/collect (:169-212): decode rows replay a captured
-                             graph of the smallest batch size >= the row count (:414-428; sizes
-                             1,2,4,8,16,32,...,max as :380-383), the other rows run one eager
-                             ragged forward (fresh prefills and continuations share the paged path).
+  * ``ModelRunner.run``    — ModelRunner::launch/collect (:169-212): decode rows go to the native
+                             decode runner (include/cppvllm_runner.h, csrc/decode_runner.cpp), which
+                             replays its HIP graph of the smallest batch size >= the row count
+                             (:414-428; sizes 1,2,4,8,16,32,...,max as :380-383); the other rows
+                             run one eager ragged forward (fresh prefills and continuations share
+                             the paged path).
 Weights are random N(0, std) bf16 (no checkpoint is loaded); norm gains are 1.
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 from dataclasses import dataclass
 
@@ -27,7 +30,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from . import ops
+from . import _lib, ops
 
 fused = ops.fused
 
@@ -229,9 +232,28 @@ def _graph_sizes(max_batch: int) -> list[int]:
     return s
 
 
+class _Graph:
+    """A decode graph of the native runner, replayed on torch's current stream."""
+
+    def __init__(self, runner: "ModelRunner", batch: int, shared: bool):
+        self.runner, self.batch, self.shared = runner, batch, shared
+
+    def replay(self) -> None:
+        r = self.runner
+        ops.check("runner_replay", r._L.cvh_runner_replay(r._handle, self.batch, int(self.shared),
+                                                           torch.cuda.current_stream().cuda_stream))
+
+
 class ModelRunner:
     """Launches scheduled batches (cppvllm_amd.engine_core.Batch) asynchronously and collects one
     sampled token per row (-1 for rows that do not sample).
+
+    Decode rows run in the native decode runner (include/cppvllm_runner.h): it stages the rows
+    through pinned memory, runs the 28-layer forward through the library's C ABI and captures /
+    replays it as HIP graphs with the HIP runtime (engine/model_runner.cpp:327-428); this class
+    hands it the weights' and the cache's device pointers and samples its output rows. Rows that
+    are not plain decode rows (fresh prompts, chunked-prefill continuations) run one eager ragged
+    forward of Qwen3.forward.
 
     Two launch slots alternate (the reference's two-deep ring, engine/model_runner.cpp:169-212 and
     engine/llm_engine.cpp:70-113): each slot owns pinned host staging and a device buffer of the
@@ -251,25 +273,16 @@ class ModelRunner:
         self.max_tokens = Tm = max(max_num_batched_tokens, max_num_seqs)
         self.max_seqs = Sm = max_num_seqs
         self.table_width = Wm = -(-max_model_len // BS)
-        self.graph_width = Wg = graph_max_blocks or self.table_width
-        self.max_graph_batch = Bm = max_num_seqs
+        self.graph_width = graph_max_blocks or self.table_width
+        self.max_graph_batch = max_num_seqs
+        if self.max_graph_batch > GEMM_MAX_ROWS:
+            raise ValueError(f"max_num_seqs {max_num_seqs} > {GEMM_MAX_ROWS} (decode graph rows)")
         i64 = dict(dtype=torch.int64)
-        # decode-graph inputs, one int64 arena: tok | pos | cu | feed | shared blocks (int32 pairs)
-        # | tables (B x Wg)
-        self.g_off = np.cumsum([0, Bm, Bm, Bm + 1, Bm, (Bm + 1) // 2]).tolist()
-        self.g_len = self.g_off[-1] + Bm * Wg
-        self.d_garena = torch.zeros(self.g_len, device=dev, **i64)
-        o = self.g_off
-        self.g_tok, self.g_pos = self.d_garena[o[0]:o[1]], self.d_garena[o[1]:o[2]]
-        self.g_cu, self.g_feed = self.d_garena[o[2]:o[3]], self.d_garena[o[3]:o[4]]
-        self.g_shared = self.d_garena[o[4]:o[5]].view(torch.int32)
-        self.g_tab = self.d_garena[o[5]:]
         # eager inputs: tok | pos | feed | cu | sampled token rows | their batch rows | tables (S x W)
         self.e_off = np.cumsum([0, Tm, Tm, Tm, Sm + 1, Sm, Sm]).tolist()
         self.e_len = self.e_off[-1] + Sm * Wm
         self.d_earena = torch.zeros(self.e_len, device=dev, **i64)
         # per launch slot: pinned staging (StagedBuffer, utils/tensor.h:64-110), sampled tokens
-        self.h_garena = [torch.zeros(self.g_len, pin_memory=True, **i64) for _ in range(2)]
         self.h_earena = [torch.zeros(self.e_len, pin_memory=True, **i64) for _ in range(2)]
         self.h_temps = [torch.zeros(Sm, pin_memory=True, dtype=torch.float32) for _ in range(2)]
         self.d_temps = torch.zeros(Sm, device=dev, dtype=torch.float32)
@@ -280,23 +293,111 @@ class ModelRunner:
         self.slot, self.last_slot = 0, None
         self.seed, self.sample_step = seed, 0
         self.ws_eager = ops.paged_attention_workspace(Tm, c.n_heads, c.n_kv_heads, c.head_dim, Wm, BS, 0, dev)
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.graphs_shared: dict[int, torch.cuda.CUDAGraph] = {}
+        self.graphs: dict[int, _Graph] = {}
+        self.graphs_shared: dict[int, _Graph] = {}
         self.shared_replays = 0
         # decode graph replays and the keys their real rows attend over (for per-launch byte counts)
         self.decode_replays = 0
         self.decode_rows = 0
         self.decode_keys = 0
-        # decode rows run the same forward with or without graphs: padded to a batch size of
-        # _graph_sizes, planned attention over the graph workspace (so a replay and an eager run of a
-        # decode step give the same bits)
+        # decode rows: padded to a batch size of _graph_sizes, planned attention (a replay and an
+        # eager run of a decode step give the same bits)
         self.graph_sizes = _graph_sizes(self.max_graph_batch)
-        Bmax = self.graph_sizes[-1]
-        self.ws_graph = ops.paged_attention_workspace(Bmax, c.n_heads, c.n_kv_heads, c.head_dim, Wg, BS, 0, dev)
-        self.g_hidden = torch.empty((Bmax, c.dim), dtype=torch.bfloat16, device=dev)
+        self.g_hidden = torch.empty((self.graph_sizes[-1], c.dim), dtype=torch.bfloat16, device=dev)
+        self._L = _lib.lib()
+        self._handle = None
+        self._create_native()
         if not enforce_eager:
             self.capture_graphs()
         self.warm_sampler()
+
+    # ---- the native decode runner ----------------------------------------------------------------
+    def _create_native(self) -> None:
+        """Describe the model and cache to cvh_runner_create. The runner keeps the device pointers:
+        the tensors are referenced here for its lifetime (call again after replacing weights)."""
+        m, c, cache = self.model, self.model.cfg, self.cache
+        fused = m.fused_ok and m.fused_epilogues
+        layers = (_lib.RunnerLayer * c.n_layers)()
+        keep = []
+        for li in range(c.n_layers):
+            kc, vc, ks, vs = cache.layers[li]
+            ts = dict(w_qkv=m.wqkv[li], w_qkv_folded=m.wqkv_f[li], w_o=m.wo[li], w_gate_up=m.w_gu[li],
+                      w_gate_up_folded=m.w_gu_f[li] if fused else None, w_down=m.w_down[li],
+                      attn_norm=m.attn_norm[li], ffn_norm=m.ffn_norm[li], q_norm=m.q_norm[li], k_norm=m.k_norm[li],
+                      k_cache=kc, v_cache=vc, k_scale=ks, v_scale=vs)
+            for k, t in ts.items():
+                if t is not None:
+                    if not t.is_contiguous():
+                        raise ValueError(f"runner: {k} of layer {li} is not contiguous")
+                    keep.append(t)
+                setattr(layers[li], k, None if t is None else t.data_ptr())
+        if not m.gate_up_interleaved:
+            raise ValueError("runner: the decode graphs need gate/up rows interleaved by 16 (2I % 32 == 0)")
+        desc = _lib.RunnerDesc(
+            n_layers=c.n_layers, dim=c.dim, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads, head_dim=c.head_dim,
+            intermediate=c.intermediate_size, vocab=c.vocab_size, norm_eps=c.norm_eps, attn_scale=m.scale,
+            block_size=cache.block_size, scale_mode=_lib.SCALE_PER_TOKEN_HEAD, max_batch=self.graph_sizes[-1],
+            table_width=self.graph_width, scratch_block=cache.scratch_block,
+            fused_min_rows=FUSED_MIN_ROWS if fused else 1, fused_max_rows=GEMM_MAX_ROWS if fused else 0,
+            embed=m.embed.data_ptr(), final_norm=m.final_norm.data_ptr(), unit_gain=m.unit_gain.data_ptr(),
+            rope_cos=m.cos.data_ptr(), rope_sin=m.sin.data_ptr(), hidden=self.g_hidden.data_ptr(), layers=layers)
+        keep += [m.embed, m.final_norm, m.unit_gain, m.cos, m.sin, self.g_hidden]
+        self.close()
+        h = C.c_void_p()
+        torch.cuda.synchronize()
+        ops.check("runner_create", self._L.cvh_runner_create(C.byref(desc), C.byref(h)))
+        self._handle, self._keep = h, keep
+        self.graphs.clear()
+        self.graphs_shared.clear()
+
+    def close(self) -> None:
+        """Free the native runner (its graphs, inputs and activations)."""
+        if getattr(self, "_handle", None) is not None:
+            torch.cuda.synchronize()
+            self._L.cvh_runner_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _stage_graph_rows(self, toks, pos, tables, B: int, feed=None, slot: int = 0, shared=None) -> None:
+        """Rows [0, S) are the decode rows; [S, B) are idle rows on the scratch block at position 0
+        with kv_len 1 (model_runner.cpp:327-357). One host-to-device copy, then the feed of tokens
+        from the previous step's samples where feed >= 0 (cvh_runner_stage)."""
+        S = len(toks)
+        i64 = lambda a: np.ascontiguousarray(a, dtype=np.int64)  # noqa: E731
+        t, p = i64(toks), i64(pos)
+        tab = i64(tables) if S else np.zeros((0, 1), np.int64)
+        f = i64(feed) if feed is not None and S else None
+        sh = np.ascontiguousarray(shared, dtype=np.int32) if shared is not None and S else None
+        prev = None
+        if f is not None and bool((f >= 0).any()):
+            prev = self._prev_sampled().data_ptr()
+        ptr = lambda a: None if a is None else a.ctypes.data  # noqa: E731
+        ops.check("runner_stage", self._L.cvh_runner_stage(
+            self._handle, slot, S, B, ptr(t), ptr(p), ptr(tab), tab.shape[1] if tab.ndim == 2 else 1, ptr(f), ptr(sh),
+            prev, torch.cuda.current_stream().cuda_stream))
+
+    def decode_eager(self, B: int, shared: bool = False) -> None:
+        """The decode forward of the staged rows, launched eagerly (the body the graphs hold)."""
+        ops.check("runner_forward", self._L.cvh_runner_forward(self._handle, B, int(shared),
+                                                                torch.cuda.current_stream().cuda_stream))
+
+    def capture_graphs(self) -> None:
+        """One graph per batch size of _graph_sizes, plain and shared-prefix variants (captured by
+        the native runner on its own stream; model_runner.cpp:371-405)."""
+        empty = np.zeros((0, self.graph_width), dtype=np.int64)
+        torch.cuda.synchronize()
+        for shared, dst in ((False, self.graphs), (True, self.graphs_shared)):
+            for B in reversed(self.graph_sizes):
+                self._stage_graph_rows([], [], empty, B)
+                torch.cuda.synchronize()
+                ops.check("runner_capture", self._L.cvh_runner_capture(self._handle, B, int(shared)))
+                dst[B] = _Graph(self, B, shared)
+        torch.cuda.synchronize()
 
     def warm_sampler(self) -> None:
         """Run the lm_head + sampler once per row count above LM_HEAD_MAX_ROWS (up to the
@@ -306,65 +407,6 @@ class ModelRunner:
         dev = self.model.device
         for S in range(LM_HEAD_MAX_ROWS + 1, self.max_seqs + 1):
             self.model.sample(torch.zeros((S, c.dim), dtype=torch.bfloat16, device=dev), self.d_tmp[:S])
-        torch.cuda.synchronize()
-
-    # ---- decode graphs -------------------------------------------------------------------------
-    def _stage_graph_rows(self, toks, pos, tables, B: int, feed=None, slot: int = 0, shared=None) -> bool:
-        """Rows [0, S) are the decode rows; [S, B) are idle rows on the scratch block at position 0
-        with kv_len 1 (model_runner.cpp:327-357). One host-to-device copy. Returns whether any
-        token must be fed from the previous step's samples."""
-        S = len(toks)
-        Wg, o = self.graph_width, self.g_off
-        h = self.h_garena[slot].numpy()
-        h[o[0]:o[0] + S], h[o[1]:o[1] + S] = toks, pos
-        h[o[0] + S:o[0] + B], h[o[1] + S:o[1] + B] = 0, 0
-        h[o[2]:o[2] + B + 1] = np.arange(B + 1)
-        need_feed = feed is not None and bool((feed >= 0).any())
-        if need_feed:
-            h[o[3]:o[3] + S] = feed
-        sh = h[o[4]:o[5]].view(np.int32)
-        sh[:B] = 0
-        if shared is not None and S:
-            sh[:S] = shared
-        tab = h[o[5]:o[5] + B * Wg].reshape(B, Wg)
-        tab[:] = -1
-        if S:
-            w = min(tables.shape[1], Wg)
-            tab[:S, :w] = tables[:, :w]
-        tab[S:B, 0] = self.cache.scratch_block
-        n = o[5] + B * Wg
-        self.d_garena[:n].copy_(self.h_garena[slot][:n], non_blocking=True)
-        return need_feed
-
-    def _graph_body(self, B: int, ws, shared: bool = False) -> None:
-        Wg = self.graph_width
-        x = self.model.forward(self.cache, self.g_tok[:B], self.g_pos[:B], self.g_cu[:B + 1],
-                               self.g_tab[:B * Wg].view(B, Wg), ws, planned=True,
-                               shared_blocks=self.g_shared[:B] if shared else None)
-        self.g_hidden[:B].copy_(x)
-
-    def capture_graphs(self) -> None:
-        sizes = self.graph_sizes
-        Bmax = sizes[-1]
-        empty = np.zeros((0, self.graph_width), dtype=np.int64)
-        self._stage_graph_rows([], [], empty, Bmax)
-        torch.cuda.synchronize()
-        pool = torch.cuda.graph_pool_handle()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            # per batch size: the plain decode graph, and a variant whose attention reads the rows'
-            # shared prefix blocks cache-resident (replayed when some decode row shares blocks)
-            for shared, dst in ((False, self.graphs), (True, self.graphs_shared)):
-                for B in reversed(sizes):
-                    for _ in range(2):
-                        self._graph_body(B, self.ws_graph, shared)
-                    side.synchronize()
-                    g = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(g, pool=pool, stream=side):
-                        self._graph_body(B, self.ws_graph, shared)
-                    dst[B] = g
-        torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
 
     # ---- sampling --------------------------------------------------------------------------------
@@ -447,16 +489,13 @@ class ModelRunner:
             B = next(b for b in self.graph_sizes if b >= n)
             shared = None if batch.shared_blocks is None else batch.shared_blocks[d0:d1]
             any_shared = shared is not None and bool((shared > 0).any())
-            need_feed = self._stage_graph_rows(batch.tokens[t0], batch.positions[t0], batch.block_tables[d0:d1], B,
-                                               None if feed is None else feed[t0], slot,
-                                               shared if any_shared else None)
-            if need_feed:
-                fused.feed_tokens(self.g_tok[:n], self.g_feed[:n], self._prev_sampled())
+            self._stage_graph_rows(batch.tokens[t0], batch.positions[t0], batch.block_tables[d0:d1], B,
+                                   None if feed is None else feed[t0], slot, shared if any_shared else None)
             graphs = self.graphs_shared if any_shared else self.graphs
             if graphs:
                 graphs[B].replay()
             else:
-                self._graph_body(B, self.ws_graph, any_shared)
+                self.decode_eager(B, any_shared)
             self.shared_replays += int(any_shared)
             self.decode_replays += 1
             self.decode_rows += n

@@ -13,7 +13,9 @@ from cppvllm_amd import _lib
 
 # host functions that write to host memory through their pointers, and argument-free queries
 SKIP = {"cvh_rope_tables_host", "cvh_gemm_bf16_nt_configs", "cvh_gemm_bf16_nt_swiglu_configs",
-        "cvh_gemm_fused_configs", "cvh_version"}
+        "cvh_gemm_fused_configs", "cvh_version",
+        # the runner's create / stage read and write host structs and arrays through their pointers
+        "cvh_runner_create", "cvh_runner_stage"}
 I64 = [-(1 << 40), -1, 0, 1, 2, 3, 16, 63, 64, 65, 255, 4097, 8192, 8193, 1 << 20, 1 << 31, 1 << 40]
 I32 = [-7, -1, 0, 1, 2, 3, 4, 8, 16, 24, 64, 96, 128, 256, 1000, 1024, 4096, 8192, 1 << 30, (1 << 31) - 1]
 # pure queries: they return a size, a count or a configuration code, not a status

@@ -15,9 +15,9 @@ steps reach the B = 256 graph, the 256-row fused epilogues and the lm_head above
   ~1.5e-2 mean-abs on rows of unit RMS. The engine must stay within FLOOR_X times that measured
   floor of the first one (it rounds more often: e.g. softmax probabilities to bf16 for the MFMA PV
   product), where a wrong position, scale or layout gives errors of order one.
-* A replayed decode graph equals the same decode step run eagerly (the runner's eager decode runs
-  the graph body itself: same padding rows, plan and partitions), bit for bit, at B = 32 and
-  B = 256 over several teacher-forced steps.
+* A replayed decode graph equals the same decode step run eagerly (the native runner's eager
+  forward is the body its graphs hold: same padding rows, plan and partitions), bit for bit, at
+  B = 32 and B = 256 over several teacher-forced steps.
 """
 import numpy as np
 import pytest
@@ -202,7 +202,7 @@ def test_config5_graph_decode_equals_eager_decode(engine, S):
         for t, s0 in zip((cache.k, cache.v, cache.ks, cache.vs), snap):
             t.copy_(s0)
         r._stage_graph_rows(cur, pos, tab, B)
-        r._graph_body(B, r.ws_graph)
+        r.decode_eager(B)
         xe = r.g_hidden[:S].clone()
         torch.cuda.synchronize()
         assert torch.equal(xg.view(torch.int16), xe.view(torch.int16)), f"step {step}: hidden rows differ"

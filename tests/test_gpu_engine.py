@@ -11,6 +11,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from cppvllm_amd import ops
 from cppvllm_amd.engine_core import Batch
 from cppvllm_amd.llm_engine import EngineConfig, LLMEngine, SamplingParams
 from cppvllm_amd.runner import Qwen3Config
@@ -228,6 +229,54 @@ def test_graph_decode_equals_eager_decode():
     assert torch.equal(k_after_graph[:, :nb], eng.cache.k[:, :nb])
     err = (xg - xe).abs()
     assert err.max().item() < 0.1 and err.mean().item() < 5e-3, (err.max().item(), err.mean().item())
+
+
+@pytest.mark.parametrize("S,B", [(3, 4), (20, 32)])
+def test_native_decode_equals_python_forward(S, B):
+    """The native decode runner (include/cppvllm_runner.h) and the Python Qwen3.forward over the same
+    staged rows (idle rows on the scratch block, planned attention) launch the same kernels with
+    the same arguments: hidden rows and cache bytes bit-identical, graph replay and eager forward,
+    unfused (B = 4) and fused-epilogue (B = 32) layers."""
+    say(f"runner: native decode vs Python forward, {S} rows in a batch of {B}")
+    eng = _engine(max_num_seqs=32, blocks=128)
+    r, m, cache = eng.runner, eng.model, eng.cache
+    g = torch.Generator().manual_seed(27)
+    lens = torch.randint(1, 200, (S,), generator=g).tolist()
+    b = _batch(lens, [0] * S, 16)
+    b.tokens[:] = torch.randint(0, SMALL.vocab_size, (b.num_tokens,), generator=g).numpy()
+    r._run_eager(b.tokens, b.positions, b.cu_seqlens, b.block_tables, np.array([], np.int64), None)
+    d = _batch([1] * S, lens, 16)
+    d.tokens[:] = torch.randint(0, SMALL.vocab_size, (S,), generator=g).numpy()
+    snap = [t.clone() for t in (cache.k, cache.v, cache.ks, cache.vs)]
+    outs = {}
+    for how in ("replay", "eager", "python"):
+        for t, s0 in zip((cache.k, cache.v, cache.ks, cache.vs), snap):
+            t.copy_(s0)
+        if how == "python":
+            Wg = r.graph_width
+            tab = np.full((B, Wg), -1, np.int64)
+            w = min(Wg, d.block_tables.shape[1])
+            tab[:S, :w] = d.block_tables[:, :w]
+            tab[S:, 0] = cache.scratch_block
+            pad = lambda a: np.concatenate([a, np.zeros(B - S, np.int64)])  # noqa: E731
+            dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)  # noqa: E731
+            ws = ops.paged_attention_workspace(B, m.cfg.n_heads, m.cfg.n_kv_heads, m.cfg.head_dim, Wg,
+                                               cache.block_size, 0, DEV)
+            x = m.forward(cache, dv(pad(d.tokens)), dv(pad(d.positions)), dv(np.arange(B + 1)), dv(tab), ws,
+                          planned=True)
+        else:
+            r._stage_graph_rows(d.tokens, d.positions, d.block_tables, B)
+            if how == "replay":
+                r.graphs[B].replay()
+            else:
+                r.decode_eager(B)
+            x = r.g_hidden[:B]
+        torch.cuda.synchronize()
+        outs[how] = (x[:S].clone(), [t.clone() for t in (cache.k, cache.v, cache.ks, cache.vs)])
+    for how in ("eager", "python"):
+        assert torch.equal(outs[how][0].view(torch.int16), outs["replay"][0].view(torch.int16)), how
+        for a, c in zip(outs[how][1], outs["replay"][1]):
+            assert torch.equal(a, c), how
 
 
 def test_eager_engine_equals_graph_engine():
