@@ -423,7 +423,7 @@ def main():
     ap.add_argument("--tp", type=int, default=1, choices=(1, 2, 4, 8),
                     help="configs 3/4 at one GPU's tensor-parallel share: kv heads 8/tp, query heads 16/tp")
     ap.add_argument("--no-shared-reuse", action="store_true",
-                    help="config 4b without telling the plan which blocks are shared (all reads non-temporal)")
+                    help="config 4b without telling the plan which blocks are shared (every sequence reads its prefix)")
     ap.add_argument("--e2e", action="store_true", help="config 5: end-to-end generation tok/s through the engine")
     ap.add_argument("--e2e-requests", type=int, default=256)
     ap.add_argument("--prefill", action="store_true", help="time the MFMA multi-query (prefill) kernel alone")
@@ -489,7 +489,9 @@ def main():
         else:
             layers.append(tuple(x.clone() for x in (b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"])))
     lib = _lib.lib()
-    ws_bytes = lib.cvh_paged_attention_workspace_bytes(T, H, KV, HD, W, BS, args.partitions)
+    shared = args.shared_prefix and not args.no_shared_reuse and not args.unplanned
+    ws_fn = lib.cvh_paged_attention_workspace_bytes_shared if shared else lib.cvh_paged_attention_workspace_bytes
+    ws_bytes = ws_fn(T, H, KV, HD, W, BS, args.partitions)
     ws = torch.zeros(max(ws_bytes, 4), dtype=torch.uint8, device=dev)
     out = torch.empty_like(b["q"])
     layer_ptrs = [tuple(x.data_ptr() for x in lay) for lay in layers]
@@ -501,7 +503,8 @@ def main():
         split_fn = lib.cvh_paged_attention_fp8_planned_split_phase
     if planned and args.shared_prefix and not args.no_shared_reuse:
         split_fn = lib.cvh_paged_attention_fp8_planned_shared_split_phase
-    merge_fn = lib.cvh_paged_attention_fp8_merge_phase
+    merge_fn = lib.cvh_paged_attention_fp8_planned_shared_merge_phase if shared else \
+        lib.cvh_paged_attention_fp8_merge_phase
 
     def launch(fn, lp):
         sp = torch.cuda.current_stream(dev).cuda_stream      # the capture stream during capture
@@ -511,11 +514,10 @@ def main():
         if code:
             raise _lib.CvhError("paged_attention_fp8", code)
 
-    shared = args.shared_prefix and not args.no_shared_reuse and planned
 
     def plan():
         sp = torch.cuda.current_stream(dev).cuda_stream
-        if shared:        # config 4b: the shared prefix blocks are read cache-resident
+        if shared:        # config 4b: the shared prefix is read once per unit of up to 8 sequences
             code = lib.cvh_paged_attention_plan_shared(b["block_tables"].data_ptr(), W, b["token_seq"].data_ptr(),
                                                        b["token_kv_len"].data_ptr(), b["shared_blocks"].data_ptr(), T,
                                                        H, KV, HD, BS, args.partitions, ws.data_ptr(), ws_bytes, sp)

@@ -51,6 +51,8 @@ SIGNATURES = {
                                                      i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned_shared_split_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32,
                                                                  i32, i32, i32, f64, i32, vp, sz, vp]),
+    "cvh_paged_attention_fp8_planned_shared_merge_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32,
+                                                                 i32, i32, i32, f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32, i32, i32,
                                               f64, i32, vp, sz, vp]),
     "cvh_paged_attention_fp8_planned_split_phase": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, vp, vp, i64, i32, i32, i32,
@@ -59,6 +61,7 @@ SIGNATURES = {
                                               f64, i32, vp]),
     "cvh_paged_attention_noalloc_max_workspace": (sz, []),
     "cvh_paged_attention_workspace_bytes": (sz, [i64, i32, i32, i32, i64, i32, i32]),
+    "cvh_paged_attention_workspace_bytes_shared": (sz, [i64, i32, i32, i32, i64, i32, i32]),
     "cvh_paged_attention_partitions": (i32, [i64, i32, i32, i32, i64, i32]),
     "cvh_rms_norm": (i32, [vp, vp, vp, i64, i32, f64, i32, vp]),
     "cvh_add_rms_norm": (i32, [vp, vp, vp, vp, i64, i32, f64, i32, vp]),

@@ -177,7 +177,8 @@ extern "C" int cvh_runner_create(const cvh_runner_desc* desc, cvh_runner** out) 
     for (int i = 0; i < 6; ++i) r->off[i] = (i ? r->off[i - 1] + lens[i - 1] : 0);
     r->arena_len = r->off[5] + lens[5];
     const int D = desc->dim, HD = desc->head_dim, H = desc->n_heads;
-    r->ws_bytes = cvh_paged_attention_workspace_bytes(Bm, H, desc->n_kv_heads, HD, W, desc->block_size, 0);
+    // the shared-prefix layout: the shared graphs plan prefix-sharing units in the same workspace
+    r->ws_bytes = cvh_paged_attention_workspace_bytes_shared(Bm, H, desc->n_kv_heads, HD, W, desc->block_size, 0);
     int rc = CVH_OK;
     auto dmalloc = [&](auto** p, size_t bytes) {
         if (rc == CVH_OK && hipMalloc(reinterpret_cast<void**>(p), std::max<size_t>(bytes, 256)) != hipSuccess) {

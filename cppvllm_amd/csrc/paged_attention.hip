@@ -245,12 +245,35 @@ struct PlanRec {
     int pad[3];
 };
 
+constexpr int kUnitTokens = 8;             // member tokens per shared-prefix unit (16 MFMA columns at GQA 2)
+struct UnitRec {
+    int seq;                               // block-table row of the group's first member
+    int keys;                              // shared keys (a multiple of the block size, or a whole context)
+    int n;                                 // member tokens in this unit
+    int tok[kUnitTokens];
+    int pad;
+};
+
 struct Params {
     uint16_t* out;
     const PlanRec* plan;     // [G] (planned launches)
     int2* plan_tok;          // [T] (kv_len, block-table row) per token, written by the plan kernel
     int* shared_tok;         // [T] keys of token t in blocks shared with another sequence (plan kernel)
     const int32_t* shared_blocks;   // [table rows] leading shared blocks per row (plan input), or null
+    // Shared-prefix units (planned shared launches at head_dim 128, GQA 2, one row group per token):
+    // sequences whose block tables start with the same shared blocks are grouped; each group's
+    // shared keys are read once per unit of up to 8 member tokens (16 MFMA columns: 8 tokens x 2
+    // query heads per kv head), and each member's own row starts after them.
+    UnitRec* units;          // [max_units] unit records (plan output)
+    int* unit_count;         // [1] number of units (plan output)
+    int2* tok_unit;          // [T] (unit, column) of a member token, (-1, 0) otherwise
+    float* ptok_acc;         // [T][H][HD] partial of a member token's own row when one range held all of it
+    float* ptok_ml;          // [T][H][2]
+    float* punit_acc;        // [max_units][WPG][16][HD] partial of a unit held whole by one range
+    float* punit_ml;         // [max_units][WPG][16][2]
+    float* psh_acc;          // [G][2][WPG][16][HD] partials of units cut by a range boundary
+    float* psh_ml;           // [G][2][WPG][16][2]
+    int max_units;
     float* part_acc;         // [G][2][WPG][REP][HD]
     float* part_ml;          // [G][2][WPG][REP][2]
     int* prefix_out;         // [rows + 1] row tile prefix, written by workgroup 0 for the merge
@@ -305,19 +328,23 @@ inline int virtual_kv_split(int rep, int head_dim) { return (rep > 2 && head_dim
 // Token metadata and the exclusive prefix of row tile counts into LDS (prefix[0..rows]); all
 // threads of the block. kv_len and the block-table row of every token are fetched together (one
 // memory round trip), so later lookups of a piece's token read LDS.
-__device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int hg_count, int* prefix, int2* tok) {
-    __shared__ int wave_tot[16];
-    const int nthreads = blockDim.x;
-    const int tid = threadIdx.x;
-    for (int t = tid; t < p.num_tokens; t += nthreads) {
+__device__ __forceinline__ void fill_tokens(const Params& p, int2* tok) {
+    for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) {
         const int64_t sq = p.token_seq[t];
         tok[t] = make_int2(token_len(p, t, sq), static_cast<int>(sq > 0 ? sq : 0));
     }
     __syncthreads();
+}
+// Exclusive prefix of the tile counts ntiles(r) of rows [0, rows) into LDS (prefix[0..rows]).
+template <typename F>
+__device__ __forceinline__ void scan_rows(int rows, F ntiles, int* prefix) {
+    __shared__ int wave_tot[16];
+    const int nthreads = blockDim.x;
+    const int tid = threadIdx.x;
     const int per = (rows + nthreads - 1) / nthreads;
     const int beg = min(rows, tid * per), end = min(rows, beg + per);
     int s = 0;
-    for (int r = beg; r < end; ++r) s += (tok[r / hg_count].x + kTileKeys - 1) / kTileKeys;
+    for (int r = beg; r < end; ++r) s += ntiles(r);
     // inclusive scan over the wave
     const int lane = tid & 63, wv = tid >> 6;
     int incl = s;
@@ -333,7 +360,7 @@ __device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int 
     int run = off + incl - s;            // exclusive prefix of this thread's chunk
     for (int r = beg; r < end; ++r) {
         prefix[r] = run;
-        run += (tok[r / hg_count].x + kTileKeys - 1) / kTileKeys;
+        run += ntiles(r);
     }
     if (tid == nthreads - 1) {
         int tot = 0;
@@ -341,6 +368,109 @@ __device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int 
         prefix[rows] = tot;
     }
     __syncthreads();
+}
+__device__ __forceinline__ void build_row_prefix(const Params& p, int rows, int hg_count, int* prefix, int2* tok) {
+    fill_tokens(p, tok);
+    scan_rows(rows, [&](int r) { return (tok[r / hg_count].x + kTileKeys - 1) / kTileKeys; }, prefix);
+}
+
+// Shared-prefix units (plan kernel, one workgroup). A token whose block-table row starts with
+// blocks other rows also hold (shared_blocks) has s = min(kv_len, shared_blocks * block_size)
+// shared keys. Tokens with the same first physical block, the same s and the same first
+// ceil(s / block_size) table entries form a group; a group of two or more is split in token order
+// into units of up to kUnitTokens members. Each member's own row then covers keys [s, kv_len)
+// only (tok.x -= s; shared_tok = s), and unit u becomes row rows_real + u of the tile space, with
+// ceil(s / 32) tiles over the group's shared keys. Returns the number of units.
+__device__ int build_units(const Params& p, int2* tok) {
+    __shared__ int n_units;
+    const int T = p.num_tokens, tid = threadIdx.x, nth = blockDim.x;
+    const int log2_bs = p.log2_bs;
+    const int64_t W = p.table_width;
+    if (tid == 0) n_units = 0;
+    for (int i = tid; i < p.max_units; i += nth) p.units[i].n = 0;
+    auto keys_of = [&](int t) -> int {
+        const int64_t nb = p.shared_blocks[tok[t].y];
+        return static_cast<int>(min(static_cast<int64_t>(tok[t].x), max(nb, int64_t{0}) << log2_bs));
+    };
+    auto same_prefix = [&](int a, int b, int keys) {
+        const int64_t* ta = p.block_tables + static_cast<int64_t>(tok[a].y) * W;
+        const int64_t* tb = p.block_tables + static_cast<int64_t>(tok[b].y) * W;
+        const int nb = (keys + (1 << log2_bs) - 1) >> log2_bs;
+        for (int i = 0; i < nb; ++i)
+            if (ta[i] != tb[i]) return false;
+        return true;
+    };
+    // pass 1: the group leader of every token (the first token with the same key), or -1
+    for (int t = tid; t < T; t += nth) {
+        const int st = (p.token_seq[t] >= 0) ? keys_of(t) : 0;
+        int lead = -1;
+        if (st > 0) {
+            const int64_t first = p.block_tables[static_cast<int64_t>(tok[t].y) * W];
+            for (int u = 0; u <= t && lead < 0; ++u)
+                if (p.token_seq[u] >= 0 && keys_of(u) == st &&
+                    p.block_tables[static_cast<int64_t>(tok[u].y) * W] == first && same_prefix(u, t, st))
+                    lead = u;
+        }
+        p.tok_unit[t] = make_int2(lead, 0);
+    }
+    __syncthreads();
+    // pass 2: index within the group; the leader also counts its group
+    for (int t = tid; t < T; t += nth) {
+        const int lead = p.tok_unit[t].x;
+        int j = 0, size = 0;
+        if (lead >= 0) {
+            for (int u = lead; u < T; ++u)
+                if (p.tok_unit[u].x == lead) {
+                    if (u < t) ++j;
+                    ++size;
+                }
+        }
+        p.shared_tok[t] = (lead == t) ? size : 0;
+        p.tok_unit[t].y = j;
+    }
+    __syncthreads();
+    // pass 3: unit ids (units ordered by leader token, then member index)
+    int my_unit[8], my_col[8], my_keys[8];
+    int k = 0;
+    for (int t = tid; t < T; t += nth, ++k) {
+        const int lead = p.tok_unit[t].x;
+        my_unit[k & 7] = -1;
+        my_col[k & 7] = 0;
+        my_keys[k & 7] = 0;
+        if (lead < 0 || p.shared_tok[lead] < 2) continue;
+        int base = 0;
+        for (int u = 0; u < lead; ++u)
+            if (p.tok_unit[u].x == u && p.shared_tok[u] >= 2) base += (p.shared_tok[u] + kUnitTokens - 1) / kUnitTokens;
+        const int j = p.tok_unit[t].y;
+        my_unit[k & 7] = base + j / kUnitTokens;
+        my_col[k & 7] = j % kUnitTokens;
+        my_keys[k & 7] = keys_of(t);
+        if (lead == t) atomicAdd(&n_units, (p.shared_tok[t] + kUnitTokens - 1) / kUnitTokens);
+    }
+    __syncthreads();
+    k = 0;
+    for (int t = tid; t < T; t += nth, ++k) {
+        const int u = my_unit[k & 7];
+        p.tok_unit[t] = make_int2(u, my_col[k & 7]);
+        p.shared_tok[t] = u >= 0 ? my_keys[k & 7] : 0;
+        if (u >= 0) {
+            UnitRec& rec = p.units[u];
+            rec.tok[my_col[k & 7]] = t;
+            if (my_col[k & 7] == 0) {
+                rec.seq = tok[t].y;
+                rec.keys = my_keys[k & 7];
+            }
+            tok[t].x -= my_keys[k & 7];
+        }
+    }
+    __syncthreads();
+    // member counts of the units (a unit's members are the columns written above)
+    for (int t = tid; t < T; t += nth) {
+        const int2 tu = p.tok_unit[t];
+        if (tu.x >= 0) atomicMax(&p.units[tu.x].n, tu.y + 1);
+    }
+    __syncthreads();
+    return n_units;
 }
 
 // First row a workgroup visits for tile range [u0, ...): the row holding tile u0, or the first
@@ -395,8 +525,11 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     extern __shared__ int prefix[];
     const int wpg = p.wpg;
     const int hg_count = p.n_kv / wpg;
-    const int rows = p.num_tokens * hg_count;
-    int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows));
+    // shared-prefix units run on the MFMA path at head_dim 128 and GQA 2 (16 columns: 8 tokens x 2 heads)
+    constexpr bool UNITS = SHARED && HD == 128 && REP == 2;
+    const int rows_real = p.num_tokens * hg_count;
+    const int rows = rows_real + ((UNITS && p.units != nullptr) ? ld_uniform(p.unit_count, 0) : 0);
+    int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows_real + p.max_units));
     // values that are the same for every lane; uniform() makes that visible to the compiler so
     // all the piece bookkeeping below stays in scalar registers
     auto uniform = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
@@ -447,8 +580,9 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         const int64_t seq = static_cast<int64_t>(uniform(static_cast<int>(pc.seq)));
         const int64_t* table = p.block_tables + seq * p.table_width;
         const int p0 = uniform(tile * kTileKeys);
+        const int off = SHARED ? uniform(pc.shared_keys) : 0;   // a member row starts after its shared keys
         if constexpr (ONE_BLOCK) {
-            const int blk = p0 >> log2_bs;
+            const int blk = (off + p0) >> log2_bs;
             if (seq != memo_seq || blk != memo_blk) {
                 memo_phys = max(ld_uniform(table, blk), int64_t{0});
                 memo_seq = seq;
@@ -456,19 +590,17 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             }
             return {memo_phys, memo_phys};
         }
-        const int64_t lo = max(ld_uniform(table, p0 >> log2_bs), int64_t{0});
-        const int64_t hi = max(ld_uniform(table, uniform(min(p0 + kTileKeys / 2, pc.kv_len - 1) >> log2_bs)),
+        const int64_t lo = max(ld_uniform(table, (off + p0) >> log2_bs), int64_t{0});
+        const int64_t hi = max(ld_uniform(table, uniform((off + min(p0 + kTileKeys / 2, pc.kv_len - 1)) >> log2_bs)),
                                int64_t{0});
         return {lo, hi};
     };
-    // Keys past kv_len (a row's last tile) are clamped to key kv_len-1: a valid, finite row whose
-    // score is masked. live = false (no work left): zero-size descriptors, no memory traffic.
-    auto load_tile_pol = [&](auto pol, const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
+    // MFMA-layout tile loads (GQA 4 / 8 rows and shared-prefix units)
+    auto mf_load = [&](auto pol, const Piece& pc, int tile, MfTile& tl, Phys ph2, bool live) {
         constexpr int POL = decltype(pol)::value;
         const int p0 = tile * kTileKeys;
         const uint32_t lv = static_cast<uint32_t>(live);             // arithmetic, not a branch
         const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
-        if constexpr (MF) {
             const uint32_t col = static_cast<uint32_t>(pc.g) * HD;   // the kv head's 128 bytes in a slot row
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -494,6 +626,16 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                     tl.vs[kb] = 1.f;
                 }
             }
+    };
+    // Keys past kv_len (a row's last tile) are clamped to key kv_len-1: a valid, finite row whose
+    // score is masked. live = false (no work left): zero-size descriptors, no memory traffic.
+    auto load_tile_pol = [&](auto pol, const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
+        constexpr int POL = decltype(pol)::value;
+        const int p0 = tile * kTileKeys;
+        const uint32_t lv = static_cast<uint32_t>(live);             // arithmetic, not a branch
+        const uint32_t kv_rec = blk_bytes32 * lv, s_rec = srow_bytes * lv;
+        if constexpr (MF) {
+            mf_load(pol, pc, tile, tl, ph2, live);
         } else {
         const uint32_t lane_col = (pc.g >> kv_shift) * HD + sub * E;   // byte column inside a slot row
 #pragma unroll
@@ -516,12 +658,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         }
     };
 
-    // wave-uniform choice of the cache policy: shared-prefix tiles stay cacheable
     auto load_tile = [&](const Piece& pc, int tile, Tile& tl, Phys ph2, bool live) {
-        if (SHARED && tile * kTileKeys < pc.shared_keys)
-            load_tile_pol(std::integral_constant<int, kTemporal>{}, pc, tile, tl, ph2, live);
-        else
-            load_tile_pol(std::integral_constant<int, kNonTemporal>{}, pc, tile, tl, ph2, live);
+        load_tile_pol(std::integral_constant<int, kNonTemporal>{}, pc, tile, tl, ph2, live);
     };
 
     Tile A, B, C;
@@ -532,7 +670,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     bool preA = false, preB = false, preQ = false;
     int plan_row = -1, plan_lt = 0, plan_rs = -1, plan_re = -1;
     constexpr int QB = REP * HD * 2;                 // bytes of one row's q slice for one wave
-    char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows, p.num_tokens) +
+    char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows_real + p.max_units, p.num_tokens) +
                     static_cast<size_t>(vg) * p.qrows * wpg * QB;
     constexpr int QL = (QB + 1023) / 1024;           // 16-byte loads per lane per row
     if constexpr (PLANNED) {
@@ -546,7 +684,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         uint4 qv[kPreQRows][QL];
 #pragma unroll
         for (int r = 0; r < kPreQRows; ++r) {
-            const bool live = r < p.qrows && plan_rs + r < plan_re;
+            const bool live = r < p.qrows && plan_rs + r < min(plan_re, rows_real);   // unit rows stage no q
             const int rr = live ? plan_rs + r : 0;
             const int t = rr / hg_count, g = (rr % hg_count) * wpg + wi;
             const auto rs = make_rsrc(p.q + (static_cast<int64_t>(t) * H + g * REP) * HD, live ? QB : 0);
@@ -591,7 +729,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             preB = b_ok;
             if (ONE_BLOCK && live) {         // the newest tile's block seeds the lookup memo
                 memo_seq = uniform(static_cast<int>(pc.seq));
-                memo_blk = ((b_ok ? plan_lt + 1 : plan_lt) * kTileKeys) >> log2_bs;
+                memo_blk = ((b_ok ? plan_lt + 1 : plan_lt) * kTileKeys + pc.shared_keys) >> log2_bs;
                 memo_phys = b_ok ? b_lo : a_lo;
             }
         }
@@ -632,7 +770,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const int r_s = PLANNED ? plan_rs : first_row(pfx, rows, u0);
     const int r_e = PLANNED ? plan_re : end_row(pfx, rows, u0, u1, r_s);
     // ---- empty rows of the range (kv_len <= 0): zero output (the reference would give 0/0)
-    for (int r = r_s; r < rows; ++r) {
+    for (int r = r_s; r < rows_real; ++r) {
         const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
         if (!(pr0 < u1 || (last_wg && pr0 == U))) break;
         if (pr1 != pr0) continue;
@@ -695,7 +833,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         }
     };
     uint32_t qf[MF ? 1 : REP][QW];
-    bf16x8_t qm[MF ? 4 : 1];                        // MFMA B operands: step st covers d = (st>>1)*64 + g*16 + (st&1)*8 .. +8
+    bf16x8_t qm[(MF || UNITS) ? 4 : 1];                        // MFMA B operands: step st covers d = (st>>1)*64 + g*16 + (st&1)*8 .. +8
     auto take_q = [&](const Piece& pc) {
         const uint16_t* src = q_lds + ((pc.row - rb) * wpg + wi) * (REP * HD);
         if constexpr (MF) {
@@ -723,7 +861,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     float m[MF ? 1 : REP], l[MF ? 1 : REP], acc[MF ? 1 : REP][E];
     // MFMA path: softmax state of this lane's S^T column (one head), O rows of heads 4g..4g+3
     float mm = kMinusHuge, lm = 0.f;
-    f32x4_t om[MF ? 8 : 1];                         // [j]: d = 8*i16 + j, rows = heads 4g..4g+3
+    f32x4_t om[(MF || UNITS) ? 8 : 1];                         // [j]: d = 8*i16 + j, rows = heads 4g..4g+3
     auto reset = [&]() {
         if constexpr (MF) {
             mm = kMinusHuge;
@@ -740,9 +878,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             }
         }
     };
-    auto compute = [&](const Piece& pc, int tile, const Tile& tl) {
+    auto mf_compute = [&](const Piece& pc, int tile, const MfTile& tl) {
         const int p0 = tile * kTileKeys;
-        if constexpr (MF) {
             // S^T for keys kb*16 + 4g + r (rows) x heads (columns)
             float sv[2][4];
 #pragma unroll
@@ -818,6 +955,11 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                     om[4 * hw + jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, vb, om[4 * hw + jj], 0, 0, 0);
                 }
             }
+    };
+    auto compute = [&](const Piece& pc, int tile, const Tile& tl) {
+        const int p0 = tile * kTileKeys;
+        if constexpr (MF) {
+            mf_compute(pc, tile, tl);
         } else {
         float sc[REP][kSteps];
 #pragma unroll
@@ -968,7 +1110,14 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 l_own = l[r];
                 m_own = m[r];
             }
-        if (pc.lt == 0 && pc.le == pr1 - pr0) {
+        if (UNITS && pc.shared_keys > 0 && pc.lt == 0 && pc.le == pr1 - pr0) {
+            // a member row held whole: its partial joins the unit's in the merge
+            const int64_t idx = (int64_t)pc.t * H + pc.g * REP + r_own;
+            float* pa = p.ptok_acc + idx * HD + sub * E + e_own;
+#pragma unroll
+            for (int i = 0; i < NV8; ++i) pa[i] = res[i];
+            if (sub == 0 && e_own == 0) reinterpret_cast<float2*>(p.ptok_ml)[idx] = make_float2(m_own, l_own);
+        } else if (pc.lt == 0 && pc.le == pr1 - pr0) {
             const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
             const float f = vfin / l_own;
             uint16_t* o = p.out + ((int64_t)pc.t * H + pc.g * REP + r_own) * HD + sub * E + e_own;
@@ -996,8 +1145,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // ---- per batch: one tile stream over its pieces, two tiles in flight ahead of the one being
     // computed (register triple buffer, unrolled by three so no tile is copied between buffers)
     for (;;) {
-        if (rb >= r_e || pfx(rb) >= u1) return;         // rlim > rb below: the loop always advances
-        const int rlim = min(r_e, rb + p.qrows);
+        if (rb >= min(r_e, rows_real) || pfx(rb) >= u1) break;   // rlim > rb below: the loop always advances
+        const int rlim = min(min(r_e, rows_real), rb + p.qrows);
         Piece pa_ = piece_from(rb, rlim);
         if (pa_.row >= 0) {
             int ta_ = pa_.lt;
@@ -1100,6 +1249,73 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         rb = rlim;
         preQ = false;
     }
+    if constexpr (UNITS) {
+        // ---- shared-prefix units of the range: each wave multiplies its kv head's K/V tiles of the
+        // group's shared keys against 16 query columns (8 member tokens x 2 heads), one pass per unit
+        // instead of one per member; the tiles are read with the default cache policy so the other
+        // units of the group find them in L2 / the last-level cache
+        if (p.units != nullptr) {
+            const auto pol = std::integral_constant<int, kTemporal>{};
+            for (int r = max(r_s, rows_real); r < r_e; ++r) {
+                const int64_t pr0 = pfx(r), pr1 = pfx(r + 1);
+                if (pr0 >= u1) break;
+                if (pr1 == pr0) continue;
+                const int u = r - rows_real;
+                const UnitRec* ur = p.units + u;
+                Piece pc;
+                pc.row = r;
+                pc.t = 0;
+                pc.g = wi;
+                pc.kv_len = ld_uniform(&ur->keys, 0);
+                pc.seq = ld_uniform(&ur->seq, 0);
+                pc.shared_keys = 0;
+                pc.lt = static_cast<int>(max(u0, pr0) - pr0);
+                pc.le = static_cast<int>(min(u1, pr1) - pr0);
+                const int n = ld_uniform(&ur->n, 0);
+                MfTile TA, TB;
+                int tile = pc.lt;
+                mf_load(pol, pc, tile, TA, lookup(pc, tile), true);
+                mf_load(pol, pc, min(tile + 1, pc.le - 1), TB, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
+                {   // column c = 2 j + h: member j's query head 2 wi + h (zero past the unit's members)
+                    const int j = i16 >> 1, hh = i16 & 1;
+                    const int tj = j < n ? ur->tok[j] : 0;
+                    const uint16_t* src = p.q + ((int64_t)tj * H + 2 * wi + hh) * HD;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                        if (j < n) v = *reinterpret_cast<const uint4*>(src + (st >> 1) * 64 + g4 * 16 + (st & 1) * 8);
+                        qm[st] = __builtin_bit_cast(bf16x8_t, v);
+                    }
+                }
+                mm = kMinusHuge;
+                lm = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) om[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                for (;;) {
+                    mf_compute(pc, tile, TA);
+                    if (++tile >= pc.le) break;
+                    mf_load(pol, pc, min(tile + 1, pc.le - 1), TA, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
+                    mf_compute(pc, tile, TB);
+                    if (++tile >= pc.le) break;
+                    mf_load(pol, pc, min(tile + 1, pc.le - 1), TB, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
+                }
+                // partials of all 16 columns: whole units in their own slot, cut ones in the range's
+                const float L = xor32_sum(xor16_sum(lm));
+                const bool whole = pc.lt == 0 && pc.le == pr1 - pr0;
+                const int64_t base = whole ? (static_cast<int64_t>(u) * wpg + wi) * 16
+                                           : ((static_cast<int64_t>(w) * 2 + (pr0 <= u0 ? 0 : 1)) * wpg + wi) * 16;
+                float* acc_b = whole ? p.punit_acc : p.psh_acc;
+                float* ml_b = whole ? p.punit_ml : p.psh_ml;
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    float* pa = acc_b + (base + 4 * g4 + rr) * HD + 8 * i16;
+                    *reinterpret_cast<float4*>(pa) = make_float4(om[0][rr], om[1][rr], om[2][rr], om[3][rr]);
+                    *reinterpret_cast<float4*>(pa + 4) = make_float4(om[4][rr], om[5][rr], om[6][rr], om[7][rr]);
+                }
+                if (g4 == 0) reinterpret_cast<float2*>(ml_b)[base + i16] = make_float2(mm, L);
+            }
+        }
+    }
 }
 
 // Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One workgroup
@@ -1110,25 +1326,44 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 // half p folds pieces w0 + p, w0 + p + 2, ... online, then half 1 hands its (M, L, A) to half 0
 // through LDS, which combines the two, so a row's chain of dependent piece loads is half as long
 // (small batches cut a row into up to 8 pieces).
+// Shared-prefix inputs of the merge (null when the launch has no units).
+struct MergeUnits {
+    const int* unit_count;
+    const int2* tok_unit;
+    const float* ptok_acc;
+    const float* ptok_ml;
+    const float* punit_acc;
+    const float* punit_ml;
+    const float* psh_acc;
+    const float* psh_ml;
+};
+
 template <int HD, int SM>
 __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
                                                           const float* __restrict__ part_ml,
                                                           const int* __restrict__ prefix,
                                                           const float* __restrict__ v_scale, int num_tokens, int n_kv,
-                                                          int rep, int wpg, int G) {
+                                                          int rep, int wpg, int G, MergeUnits mu) {
     constexpr int TPH = HD / 4;                       // threads per query head
     const int row = blockIdx.x;
     const int hg_count = n_kv / wpg;
     const int heads_per_row = wpg * rep;             // query heads of one row group
-    const int rows = num_tokens * hg_count;
-    const int64_t U = prefix[rows];
+    const int rows_real = num_tokens * hg_count;
+    const int n_units = mu.tok_unit != nullptr ? *mu.unit_count : 0;
+    const int64_t U = prefix[rows_real + n_units];
     const int64_t pr0 = prefix[row], pr1 = prefix[row + 1];
-    if (pr1 == pr0) return;
+    const int t = row / hg_count, hgi = row % hg_count;
+    // a member token of a shared-prefix unit: its own row (keys after the shared prefix) and its
+    // unit's column are merged here even when one range held either whole
+    const int2 tu = (mu.tok_unit != nullptr) ? mu.tok_unit[t] : make_int2(-1, 0);
+    const bool member = tu.x >= 0;
+    if (!member && pr1 == pr0) return;
     // workgroup holding tile u: the largest w with w*U/G <= u
     auto owner = [&](int64_t u) { return static_cast<int>(((u + 1) * G - 1) / U); };
-    const int w0 = owner(pr0), w1 = owner(pr1 - 1);
-    if (w0 == w1) return;
-    const int t = row / hg_count, hgi = row % hg_count;
+    const int w0 = pr1 > pr0 ? owner(pr0) : 0, w1 = pr1 > pr0 ? owner(pr1 - 1) : -1;
+    if (!member && w0 == w1) return;
+    const int64_t q0 = member ? prefix[rows_real + tu.x] : 0, q1 = member ? prefix[rows_real + tu.x + 1] : 0;
+    const int v0 = member ? owner(q0) : 0, v1 = member ? owner(q1 - 1) : -1;
     const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
     __shared__ float xs[6][512];
     const int half = static_cast<int>(blockDim.x) / 2, part = static_cast<int>(threadIdx.x) >= half ? 1 : 0;
@@ -1139,14 +1374,8 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
         const int d0 = ((base + ti) % TPH) * 4;
         float M = kMinusHuge, L = 0.f;
         float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-        for (int w = w0 + part; w <= w1; w += 2) {
-            // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
-            if (w * U / G == (w + 1) * U / G) continue;
-            const int slot = (pr0 <= w * U / G) ? 0 : 1;
-            const int64_t idx = (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh;
-            const float2 ml = reinterpret_cast<const float2*>(part_ml)[idx];
-            const float4 a = *reinterpret_cast<const float4*>(part_acc + idx * HD + d0);
+        auto fold = [&](float2 ml, const float* src) {
+            const float4 a = *reinterpret_cast<const float4*>(src);
             const float Mn = fmaxf(M, ml.x);
             const float co = exp2f(M - Mn), cn = exp2f(ml.x - Mn);
             L = L * co + ml.y * cn;
@@ -1155,6 +1384,38 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
             A.z = A.z * co + a.z * cn;
             A.w = A.w * co + a.w * cn;
             M = Mn;
+        };
+        const int h = hgi * heads_per_row + hh;      // query head index within the token
+        if (member && w0 == w1) {                    // the row's own keys, held whole by one range
+            if (part == 0) {
+                const int64_t idx = (int64_t)t * n_kv * rep + h;
+                fold(reinterpret_cast<const float2*>(mu.ptok_ml)[idx], mu.ptok_acc + idx * HD + d0);
+            }
+        } else {
+#pragma unroll 4
+            for (int w = w0 + part; w <= w1; w += 2) {
+                // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
+                if (w * U / G == (w + 1) * U / G) continue;
+                const int slot = (pr0 <= w * U / G) ? 0 : 1;
+                const int64_t idx = (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh;
+                fold(reinterpret_cast<const float2*>(part_ml)[idx], part_acc + idx * HD + d0);
+            }
+        }
+        if (member) {                                // the unit's column of this head
+            const int wv = hh / rep, col = 2 * tu.y + hh % rep;
+            if (v0 == v1) {
+                if (part == 0) {
+                    const int64_t idx = (static_cast<int64_t>(tu.x) * wpg + wv) * 16 + col;
+                    fold(reinterpret_cast<const float2*>(mu.punit_ml)[idx], mu.punit_acc + idx * HD + d0);
+                }
+            } else {
+                for (int w = v0 + part; w <= v1; w += 2) {
+                    if (w * U / G == (w + 1) * U / G) continue;
+                    const int slot = (q0 <= w * U / G) ? 0 : 1;
+                    const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wv) * 16 + col;
+                    fold(reinterpret_cast<const float2*>(mu.psh_ml)[idx], mu.psh_acc + idx * HD + d0);
+                }
+            }
         }
         if (part) {
             xs[0][ti] = M; xs[1][ti] = L; xs[2][ti] = A.x; xs[3][ti] = A.y; xs[4][ti] = A.z; xs[5][ti] = A.w;
@@ -1169,7 +1430,6 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
             A.z = A.z * c0 + xs[4][ti] * c1;
             A.w = A.w * c0 + xs[5][ti] * c1;
             const float f = vfin / L;
-            const int h = hgi * heads_per_row + hh;      // query head index within the token
             uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
             const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
             const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
@@ -1187,26 +1447,34 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
 __global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* plan, int G, int one_block) {
     extern __shared__ int prefix[];
     const int hg_count = p.n_kv / p.wpg;
-    const int rows = p.num_tokens * hg_count;
-    int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows));
-    build_row_prefix(p, rows, hg_count, prefix, tok);
-    for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
-    for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) {
-        p.plan_tok[t] = tok[t];
-        int sh = 0;
-        if (p.shared_blocks != nullptr) {
-            const int64_t nb = p.shared_blocks[tok[t].y];
-            sh = static_cast<int>(min(static_cast<int64_t>(tok[t].x), max(nb, int64_t{0}) << p.log2_bs));
-        }
-        p.shared_tok[t] = sh;
+    const int rows_real = p.num_tokens * hg_count;
+    // the token table sits after the largest prefix this launch may build (real rows + units)
+    int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows_real + p.max_units));
+    int rows = rows_real;
+    if (p.units != nullptr) {       // shared-prefix units: group first, then the prefix over rows + units
+        fill_tokens(p, tok);
+        const int nu = build_units(p, tok);
+        if (threadIdx.x == 0) *p.unit_count = nu;
+        rows = rows_real + nu;
+        const UnitRec* units = p.units;
+        scan_rows(rows, [&](int r) {
+            return r < rows_real ? (tok[r / hg_count].x + kTileKeys - 1) / kTileKeys
+                                 : (units[r - rows_real].keys + kTileKeys - 1) / kTileKeys;
+        }, prefix);
+    } else {
+        build_row_prefix(p, rows, hg_count, prefix, tok);
+        for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) p.shared_tok[t] = 0;
     }
+    for (int i = threadIdx.x; i <= rows; i += blockDim.x) p.prefix_out[i] = prefix[i];
+    for (int t = threadIdx.x; t < p.num_tokens; t += blockDim.x) p.plan_tok[t] = tok[t];
+    __syncthreads();
     const int64_t U = prefix[rows];
     const int log2_bs = p.log2_bs;
     auto pf = [&](int i) { return prefix[i]; };
     for (int w = threadIdx.x; w < G; w += blockDim.x) {
         const int64_t u0 = w * U / G, u1 = (w + 1) * U / G;
         const int r_s = first_row(pf, rows, u0);
-        const int rlim = min(rows, r_s + p.qrows);
+        const int rlim = min(rows_real, r_s + p.qrows);
         PlanRec rec = {};
         rec.row = -1;
         rec.r_s = r_s;
@@ -1242,10 +1510,12 @@ __global__ __launch_bounds__(1024) void paged_plan_kernel(Params p, PlanRec* pla
         }
         if (rec.row >= 0) {
             const int64_t* table = p.block_tables + static_cast<int64_t>(rec.seq) * p.table_width;
+            const int off = p.shared_tok[rec.row / hg_count];     // a member row starts after its shared keys
             auto phys = [&](int tile, int64_t& lo, int64_t& hi) {
                 const int p0 = tile * kTileKeys;
-                lo = max(table[p0 >> log2_bs], int64_t{0});
-                hi = one_block ? lo : max(table[min(p0 + kTileKeys / 2, rec.kv_len - 1) >> log2_bs], int64_t{0});
+                lo = max(table[(off + p0) >> log2_bs], int64_t{0});
+                hi = one_block ? lo
+                               : max(table[(off + min(p0 + kTileKeys / 2, rec.kv_len - 1)) >> log2_bs], int64_t{0});
             };
             phys(rec.lt, rec.a_lo, rec.a_hi);
             rec.b_ok = rec.lt + 1 < rec.le;
@@ -1292,11 +1562,16 @@ int auto_partitions(int64_t T, int n_kv, int64_t table_width, int block_size) {
 // | plan: token metadata int2 [T], shared-prefix keys int32 [T], workgroup records PlanRec [G]
 struct Workspace {
     size_t prefix_off, acc_off, ml_off, tok_off, shared_off, plan_off, total;
+    // shared-prefix units (layouts sized for shared launches only)
+    size_t units_off, ucount_off, tok_unit_off, ptok_acc_off, ptok_ml_off, punit_acc_off, punit_ml_off, psh_acc_off,
+            psh_ml_off;
+    int max_units;
 };
 size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
-Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
+int max_units_for(int64_t T) { return static_cast<int>(T / 2); }
+Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G, bool shared = false) {
     const int64_t hg = n_kv / waves_per_group(n_kv);
-    const int64_t rows = T * hg;
+    const int64_t rows = T * hg + (shared ? max_units_for(T) : 0);
     const int64_t slots = static_cast<int64_t>(G) * 2 * (n_heads / hg);   // [G][2][WPG*REP]
     Workspace w;
     w.prefix_off = 0;
@@ -1306,6 +1581,23 @@ Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G) {
     w.shared_off = w.tok_off + align256(static_cast<size_t>(T) * sizeof(int2));
     w.plan_off = w.shared_off + align256(static_cast<size_t>(T) * sizeof(int));
     w.total = w.plan_off + align256(static_cast<size_t>(G) * sizeof(PlanRec));
+    w.max_units = shared ? max_units_for(T) : 0;
+    w.units_off = w.ucount_off = w.tok_unit_off = w.ptok_acc_off = w.ptok_ml_off = w.punit_acc_off = w.punit_ml_off =
+            w.psh_acc_off = w.psh_ml_off = w.total;
+    if (shared) {
+        const size_t wpg = static_cast<size_t>(waves_per_group(n_kv));
+        const size_t mu = static_cast<size_t>(w.max_units);
+        w.units_off = w.total;
+        w.ucount_off = w.units_off + align256(mu * sizeof(UnitRec));
+        w.tok_unit_off = w.ucount_off + 256;
+        w.ptok_acc_off = w.tok_unit_off + align256(static_cast<size_t>(T) * sizeof(int2));
+        w.ptok_ml_off = w.ptok_acc_off + align256(static_cast<size_t>(T) * n_heads * HD * sizeof(float));
+        w.punit_acc_off = w.ptok_ml_off + align256(static_cast<size_t>(T) * n_heads * 2 * sizeof(float));
+        w.punit_ml_off = w.punit_acc_off + align256(mu * wpg * 16 * HD * sizeof(float));
+        w.psh_acc_off = w.punit_ml_off + align256(mu * wpg * 16 * 2 * sizeof(float));
+        w.psh_ml_off = w.psh_acc_off + align256(static_cast<size_t>(G) * 2 * wpg * 16 * HD * sizeof(float));
+        w.total = w.psh_ml_off + align256(static_cast<size_t>(G) * 2 * wpg * 16 * 2 * sizeof(float));
+    }
     return w;
 }
 
@@ -1389,12 +1681,28 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (tile_bound(num_tokens, n_kv_heads, table_width, block_size) >= (int64_t{1} << 31) / 2)
         return CVH_ERR_UNSUPPORTED;
     const int G = partitions ? partitions : auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
-    const Workspace wl = ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G);
+    // shared-prefix launches (plan_shared and the _shared launches) use the larger layout; units run
+    // where the MFMA unit path exists (head_dim 128, GQA 2, one row group per token)
+    const bool shared = (phase & kPhaseShared) || shared_blocks != nullptr;
+    const bool units_on = shared && head_dim == 128 && rep_v == 2 && n_kv_heads == wpg;
+    const Workspace wl = ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G, shared);
     if (workspace == nullptr || workspace_bytes < wl.total) return CVH_ERR_WORKSPACE;
     char* wsb = static_cast<char*>(workspace);
 
-    Params p;
+    Params p{};
     p.out = static_cast<uint16_t*>(out);
+    p.max_units = wl.max_units;
+    if (units_on) {
+        p.units = reinterpret_cast<UnitRec*>(wsb + wl.units_off);
+        p.unit_count = reinterpret_cast<int*>(wsb + wl.ucount_off);
+        p.tok_unit = reinterpret_cast<int2*>(wsb + wl.tok_unit_off);
+        p.ptok_acc = reinterpret_cast<float*>(wsb + wl.ptok_acc_off);
+        p.ptok_ml = reinterpret_cast<float*>(wsb + wl.ptok_ml_off);
+        p.punit_acc = reinterpret_cast<float*>(wsb + wl.punit_acc_off);
+        p.punit_ml = reinterpret_cast<float*>(wsb + wl.punit_ml_off);
+        p.psh_acc = reinterpret_cast<float*>(wsb + wl.psh_acc_off);
+        p.psh_ml = reinterpret_cast<float*>(wsb + wl.psh_ml_off);
+    }
     p.prefix_out = reinterpret_cast<int*>(wsb + wl.prefix_off);
     PlanRec* plan = reinterpret_cast<PlanRec*>(wsb + wl.plan_off);
     p.plan = plan;
@@ -1428,7 +1736,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         }
     {
         // q staging rows: as many as the LDS left by the row prefix and token table allows
-        const size_t fixed = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens));
+        const size_t fixed = lds_q_offset(static_cast<int>(rows) + p.max_units, static_cast<int>(num_tokens));
         const size_t per_row = static_cast<size_t>(wpg) * p.pack * rep_v * head_dim * 2;
         const int fit = fixed < kLdsBytes ? static_cast<int>((kLdsBytes - fixed) / per_row) : 0;
         if (fit < 1) return CVH_ERR_UNSUPPORTED;
@@ -1441,7 +1749,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
 
     auto s = reinterpret_cast<hipStream_t>(stream);
     if (phase & kPhasePlan) {
-        const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens));
+        const size_t lds = lds_q_offset(static_cast<int>(rows) + p.max_units, static_cast<int>(num_tokens));
         const bool one_block = (1 << lg) >= kTileKeys;
         if (lds > 65536)
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(paged_plan_kernel),
@@ -1451,7 +1759,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     }
     if (phase & kPhaseDecode) {
         const int planned = (phase & kPhasePlanned) ? ((phase & kPhaseShared) ? 2 : 1) : 0;
-        const size_t lds = lds_q_offset(static_cast<int>(rows), static_cast<int>(num_tokens)) +
+        const size_t lds = lds_q_offset(static_cast<int>(rows) + p.max_units, static_cast<int>(num_tokens)) +
                            static_cast<size_t>(p.qrows) * wpg * p.pack * rep_v * head_dim * 2;
         const int WG = G / p.pack, nth = 64 * wpg * p.pack;
         const bool one_block = (1 << lg) >= kTileKeys;
@@ -1466,7 +1774,10 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         if (!ok) return CVH_ERR_UNSUPPORTED;
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
-    if ((phase & kPhaseMerge) && G > 1) {
+    MergeUnits mu{};
+    if (units_on)
+        mu = MergeUnits{p.unit_count, p.tok_unit, p.ptok_acc, p.ptok_ml, p.punit_acc, p.punit_ml, p.psh_acc, p.psh_ml};
+    if ((phase & kPhaseMerge) && (G > 1 || units_on)) {
         const dim3 mgrid(static_cast<unsigned>(rows));
         const int nt = static_cast<int>(num_tokens);
         // two halves of one thread per (head, 4 dims) slice, at most 512 each (more slices loop)
@@ -1474,17 +1785,17 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G, mu);
             else
                 paged_merge2_kernel<128, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G, mu);
         } else {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge2_kernel<64, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G, mu);
             else
                 paged_merge2_kernel<64, CVH_SCALE_PER_TENSOR><<<mgrid, m2, 0, s>>>(
-                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G);
+                        p.out, p.part_acc, p.part_ml, p.prefix_out, v_scale, nt, n_kv_heads, rep_v, wpg, G, mu);
         }
         if (hipGetLastError() != hipSuccess) return CVH_ERR_LAUNCH;
     }
@@ -1513,6 +1824,18 @@ extern "C" size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_
     const int n_kv = n_kv_heads * cvh::virtual_kv_split(rep, head_dim);   // the kernel's kv heads, as in the launch
     const int G = partitions ? partitions : cvh::auto_partitions(num_tokens, n_kv, table_width, block_size);
     return cvh::ws_layout(num_tokens, n_heads, n_kv, head_dim, G).total;
+}
+
+extern "C" size_t cvh_paged_attention_workspace_bytes_shared(int64_t num_tokens, int n_heads, int n_kv_heads,
+                                                             int head_dim, int64_t table_width, int block_size,
+                                                             int partitions) {
+    if (num_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0 || table_width <= 0 || block_size <= 0 ||
+        partitions < 0 || n_heads % n_kv_heads != 0)
+        return 0;
+    const int rep = n_heads / n_kv_heads;
+    const int n_kv = n_kv_heads * cvh::virtual_kv_split(rep, head_dim);
+    const int G = partitions ? partitions : cvh::auto_partitions(num_tokens, n_kv, table_width, block_size);
+    return cvh::ws_layout(num_tokens, n_heads, n_kv, head_dim, G, true).total;
 }
 
 #define CVH_PA_ARGS                                                                                                  \
@@ -1546,6 +1869,9 @@ extern "C" int cvh_paged_attention_fp8_planned_shared(CVH_PA_PARAMS) {
 }
 extern "C" int cvh_paged_attention_fp8_planned_shared_split_phase(CVH_PA_PARAMS) {
     return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseDecode | cvh::kPhasePlanned | cvh::kPhaseShared);
+}
+extern "C" int cvh_paged_attention_fp8_planned_shared_merge_phase(CVH_PA_PARAMS) {
+    return cvh::paged_attention(CVH_PA_ARGS, cvh::kPhaseMerge | cvh::kPhasePlanned | cvh::kPhaseShared);
 }
 extern "C" int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
                                         const int64_t* token_kv_len, int64_t num_tokens, int n_heads, int n_kv_heads,

@@ -43,10 +43,13 @@ def _scale_mode(k_scale: torch.Tensor) -> int:
 
 
 def paged_attention_workspace(num_tokens: int, n_heads: int, n_kv_heads: int, head_dim: int, table_width: int,
-                              block_size: int, partitions: int = 0, device="cuda") -> torch.Tensor:
-    """Preallocated split-K workspace (what the reference allocates per call, paged_attention.cu:415-421)."""
-    n = _lib.lib().cvh_paged_attention_workspace_bytes(num_tokens, n_heads, n_kv_heads, head_dim, table_width,
-                                                      block_size, partitions)
+                              block_size: int, partitions: int = 0, device="cuda", shared: bool = False) -> torch.Tensor:
+    """Preallocated split-K workspace (what the reference allocates per call, paged_attention.cu:415-421).
+    shared=True: the layout of the prefix-sharing plan and launches (paged_attention_plan with
+    shared_blocks, paged_attention_fp8(..., shared=True))."""
+    L = _lib.lib()
+    fn = L.cvh_paged_attention_workspace_bytes_shared if shared else L.cvh_paged_attention_workspace_bytes
+    n = fn(num_tokens, n_heads, n_kv_heads, head_dim, table_width, block_size, partitions)
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
@@ -55,7 +58,9 @@ def paged_attention_plan(block_tables, token_seq, token_kv_len, n_heads: int, n_
                          shared_blocks: torch.Tensor | None = None) -> None:
     """Build the per-step plan that ``paged_attention_fp8(..., planned=True)`` reads from `workspace`
     (once per batch layout, before the layers of a step). shared_blocks (int32, one per table row):
-    leading blocks each row shares with other rows (prefix-cache hits), read cache-resident."""
+    leading blocks each row shares with other rows (prefix-cache hits): tokens whose rows share them
+    are grouped, and the shared launches read each group's shared K/V once per unit of up to 8
+    tokens (needs a workspace made with shared=True)."""
     T = token_seq.size(0)
     if T == 0:
         return
@@ -82,8 +87,8 @@ def paged_attention_fp8(out, q, k_cache, v_cache, k_scale, v_scale, block_tables
     out, q: bf16 [T, H, HD]; k_cache, v_cache: uint8 [NB, BS, KV, HD]; k_scale, v_scale: float32
     [NB, BS, KV] (memory order [NB][KV][BS]) or one element each (per-tensor); block_tables int64
     [S, W]; token_seq, token_kv_len int64 [T]. planned=True reads the plan that
-    ``paged_attention_plan`` left in `workspace` for the same layout; shared=True also reads the
-    shared-prefix keys of a plan built with shared_blocks (cache-resident loads of those blocks).
+    ``paged_attention_plan`` left in `workspace` for the same layout; shared=True runs the
+    shared-prefix units of a plan built with shared_blocks.
     """
     T = q.size(0)
     if T == 0:

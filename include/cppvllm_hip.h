@@ -162,11 +162,18 @@ int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, c
                              int head_dim, int block_size, int partitions, void* workspace, size_t workspace_bytes,
                              cvh_stream_t stream);
 /* cvh_paged_attention_plan with prefix-cache sharing: shared_blocks[r] (int32, one per
- * block-table row) is how many leading blocks of row r are also referenced by other rows. The
- * _planned_shared launches (same arguments as _planned) read those blocks' K/V with the default
- * cache policy (the rest non-temporal), so the first sequence to read a shared block leaves it in
- * L2 / the last-level cache for the others. Results are bitwise those of the plain plan and
- * launches; the plain _planned launches ignore the sharing (no per-tile test in their loop).
+ * block-table row) is how many leading blocks of row r are also referenced by other rows (the block
+ * manager's reference counts). Query tokens whose rows start with the same physical blocks (same
+ * first block, same shared key count s = min(kv_len, shared_blocks * block_size), same first
+ * ceil(s / block_size) table entries) form a group; a group of two or more is split in token order
+ * into units of up to 8 tokens. The _planned_shared launches (same arguments as _planned) then read
+ * each unit's shared K/V once for all its tokens (one matrix-core pass: 8 tokens x 2 query heads
+ * per kv head as 16 MFMA columns) and each token's own tiles from key s on, and the merge combines
+ * the two per token. Units run at head_dim 128 with 2 query heads per kv head and at most 8 kv
+ * heads; other shapes, and tokens in no group, run as the plain plan. Results equal the plain
+ * launches within the attention tolerance (another summation order), and are bitwise reproducible.
+ * Workspace: cvh_paged_attention_workspace_bytes_shared bytes (the plan, the _shared launches and
+ * their merge phase use the same layout).
  * (Prefix-shared block reuse; no reference counterpart: the reference re-reads shared blocks
  *  per sequence, engine/block_manager.cpp:80-116 hands out the shared ids.) */
 int cvh_paged_attention_plan_shared(const int64_t* block_tables, int64_t table_width, const int64_t* token_seq,
@@ -180,6 +187,15 @@ int cvh_paged_attention_fp8_planned_shared(void* out, const void* q, const uint8
                                            int block_size, int scale_mode, double scale, int partitions,
                                            void* workspace, size_t workspace_bytes, cvh_stream_t stream);
 int cvh_paged_attention_fp8_planned_shared_split_phase(void* out, const void* q, const uint8_t* k_cache,
+                                                       const uint8_t* v_cache, const float* k_scale,
+                                                       const float* v_scale, const int64_t* block_tables,
+                                                       int64_t table_width, const int64_t* token_seq,
+                                                       const int64_t* token_kv_len, int64_t num_tokens, int n_heads,
+                                                       int n_kv_heads, int head_dim, int block_size, int scale_mode,
+                                                       double scale, int partitions, void* workspace,
+                                                       size_t workspace_bytes, cvh_stream_t stream);
+/* Merge phase of a _planned_shared_split_phase launch (the cut rows and every unit member). */
+int cvh_paged_attention_fp8_planned_shared_merge_phase(void* out, const void* q, const uint8_t* k_cache,
                                                        const uint8_t* v_cache, const float* k_scale,
                                                        const float* v_scale, const int64_t* block_tables,
                                                        int64_t table_width, const int64_t* token_seq,
@@ -222,6 +238,10 @@ size_t cvh_paged_attention_noalloc_max_workspace(void);
  * kernels/paged_attention.cu:415-421, which cannot run under graph capture). */
 size_t cvh_paged_attention_workspace_bytes(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
                                            int64_t table_width, int block_size, int partitions);
+
+/* Workspace bytes of the prefix-sharing plan and launches (cvh_paged_attention_plan_shared). */
+size_t cvh_paged_attention_workspace_bytes_shared(int64_t num_tokens, int n_heads, int n_kv_heads, int head_dim,
+                                                  int64_t table_width, int block_size, int partitions);
 
 /* The partition count the automatic policy picks for these shapes (the same count the launches
  * and cvh_paged_attention_workspace_bytes use for partitions = 0). */

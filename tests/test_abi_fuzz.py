@@ -21,6 +21,7 @@ I32 = [-7, -1, 0, 1, 2, 3, 4, 8, 16, 24, 64, 96, 128, 256, 1000, 1024, 4096, 819
 # pure queries: they return a size, a count or a configuration code, not a status
 QUERIES = {"cvh_gemm_bf16_nt_config", "cvh_gemm_bf16_nt_swiglu_config", "cvh_gemm_fused_config",
            "cvh_paged_attention_partitions", "cvh_paged_attention_workspace_bytes",
+           "cvh_paged_attention_workspace_bytes_shared",
            "cvh_paged_attention_prefill_workspace_bytes", "cvh_paged_attention_noalloc_max_workspace"}
 F64 = [0.0, 1e-6, 0.088, 1.0, -1.0, float("inf"), float("nan")]
 SZ = [0, 16, 1 << 20, 1 << 40]

@@ -621,29 +621,6 @@ def test_prefill_kernel_agrees_with_decode_kernel(mode):
     assert_close_bf16(run_gpu(b, prefill=mode), run_gpu(b), max_abs=1.6e-2, mean_abs=1e-3)
 
 
-def test_shared_prefix_plan_is_bitwise_identical(orc):
-    """Config 4b with the shared-prefix plan (cache-resident reads of the 8 shared blocks): the
-    cache policy changes no result bit; both agree with the oracle on a sample of rows."""
-    say("config4b planned with shared_blocks vs plain plan")
-    b = workloads.config4(device=DEV, shared_prefix=True)
-    assert int(b["shared_blocks"].sum()) > 0
-    T, H, KV, HD, BS = b["q"].shape[0], b["n_heads"], b["n_kv_heads"], b["head_dim"], b["block_size"]
-    ws = ops.paged_attention_workspace(T, H, KV, HD, b["block_tables"].shape[1], BS, 0, DEV)
-    outs = []
-    for shared in (None, b["shared_blocks"]):
-        ops.paged_attention_plan(b["block_tables"], b["token_seq"], b["token_kv_len"], H, KV, HD, BS, ws,
-                                 shared_blocks=shared)
-        out = torch.empty_like(b["q"])
-        ops.paged_attention_fp8(out, b["q"], b["k_cache"], b["v_cache"], b["k_scale"], b["v_scale"],
-                                b["block_tables"], b["token_seq"], b["token_kv_len"], b["scale"], workspace=ws,
-                                planned=True, shared=shared is not None)
-        torch.cuda.synchronize()
-        outs.append(bits(out))
-    assert np.array_equal(outs[0], outs[1])
-    assert_close_bf16(outs[1], run_oracle(orc, {k: (v.cpu() if isinstance(v, torch.Tensor) else v)
-                                               for k, v in b.items()}), ulp_floor=True)
-
-
 @pytest.mark.parametrize("tp", [2, 4, 8])
 def test_tp_share_matches_full_heads(orc, tp):
     """One GPU's tensor-parallel shard of config 3 (kv heads [0, 8/tp), their query heads, the
