@@ -17,6 +17,12 @@
 //     one of two per-workgroup slots (0: the piece containing the workgroup's first tile, 1: the
 //     one containing its last); whole rows are finished in place. paged_merge2_kernel combines
 //     the pieces of cut rows.
+//   * shared-prefix units (planned shared launches): the plan groups tokens whose block tables
+//     start with the same shared blocks (prefix-cache hits) and appends one row per unit of up to
+//     8 such tokens after the real rows; a unit's tiles are the group's shared keys, multiplied on
+//     matrix cores against the 16 query columns of its tokens (8 tokens x 2 query heads), so the
+//     prefix is read once per unit instead of once per token. Members' own rows start after the
+//     shared keys; member rows and units always end as partials, which the merge combines.
 //
 // Per wave (one kv head, REP query heads), designed for wave64:
 //   * lane = (grp, sub): grp = lane/8 picks one of 8 keys of a step, sub = lane%8 owns a 16-byte
@@ -71,8 +77,8 @@ typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufferWord3);
 }
-// Blocks that several sequences share (prefix-cache hits) are read with the default policy
-// instead, so the first reader leaves them in L2 / the last-level cache for the others.
+// The shared-prefix units read their group's blocks with the default policy instead, so the
+// group's other units find them in L2 / the last-level cache.
 constexpr int kTemporal = 0;
 template <typename VT, int POL = kNonTemporal> __device__ __forceinline__ VT buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off);
 template <> __device__ __forceinline__ uint4 buf_load<uint4, kNonTemporal>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -1602,7 +1608,7 @@ Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G, bool shared
 }
 
 // kPhasePlanned: the decode phase reads the plan kPhasePlan left in the workspace
-// kPhaseShared (with kPhasePlanned): also read the plan's shared-prefix keys (cache-resident loads)
+// kPhaseShared (with kPhasePlanned): the shared-prefix layout: units and member rows of the plan
 enum Phase { kPhaseDecode = 1, kPhaseMerge = 2, kPhaseBoth = 3, kPhasePlanned = 4, kPhasePlan = 8, kPhaseShared = 16 };
 
 template <typename K>

@@ -156,7 +156,7 @@ class Qwen3:
         ops.embedding(h, self.embed, tokens)
         x = torch.empty_like(h)
         shared = planned and shared_blocks is not None
-        if planned:   # shared_blocks: per-row leading blocks shared with other rows, read cache-resident
+        if planned:   # shared_blocks: per-row leading blocks shared with other rows (shared-prefix units)
             ops.paged_attention_plan(block_tables, seq, kvl, H, KV, HD, cache.block_size, workspace,
                                      shared_blocks=shared_blocks if shared else None)
         q = torch.empty((T, H, HD), dtype=bf16, device=dev)
