@@ -157,6 +157,11 @@ extern "C" int cvh_runner_create(const cvh_runner_desc* desc, cvh_runner** out) 
     if (desc->dim % 128 != 0 || (desc->n_heads * desc->head_dim) % 128 != 0 || desc->intermediate % 128 != 0 ||
         (2 * desc->intermediate) % 32 != 0 || qkv_n % 16 != 0)
         return CVH_ERR_UNSUPPORTED;
+    // the fused-epilogue projections: 128-wide heads, rows of at most 1024 (the row-norm partials a
+    // lane sums), 256-column tiles over the hidden size, 128-column gate/up tiles
+    if (desc->fused_min_rows <= desc->fused_max_rows &&
+        (desc->head_dim != 128 || desc->dim > 1024 || (2 * desc->intermediate) % 128 != 0 || desc->fused_min_rows < 1))
+        return CVH_ERR_UNSUPPORTED;
     for (int i = 0; i < desc->n_layers; ++i) {
         const cvh_runner_layer& L = desc->layers[i];
         if (!L.w_qkv || !L.w_o || !L.w_gate_up || !L.w_down || !L.attn_norm || !L.ffn_norm || !L.q_norm || !L.k_norm ||
