@@ -248,3 +248,37 @@ def test_noalloc_array_holds_every_automatic_workspace():
                         assert 0 < n <= mx, (hd, kv, rep, T, W, bs, n)
                         worst = max(worst, n)
     assert worst > mx // 2     # the bound is tight to within a factor of two (GQA 8: ~16.5 MiB)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="passes dummy device pointers; CPU-only check")
+def test_runner_create_validates_before_allocating():
+    """cvh_runner_create rejects bad descriptions before any device call: missing pointers,
+    shapes the decode projections do not take, and fused-epilogue windows on shapes the fused
+    projections do not take; handles it did not hand out are refused by every runner entry point."""
+    lib = _lib.lib()
+    L = 2
+    layers = (_lib.RunnerLayer * L)()
+    for i in range(L):
+        for name, _ in _lib.RunnerLayer._fields_:
+            setattr(layers[i], name, 4096)
+    def desc(**kw):
+        d = dict(n_layers=L, dim=1024, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=3072, vocab=151936,
+                 norm_eps=1e-6, attn_scale=0.088, block_size=256, scale_mode=0, max_batch=32, table_width=8,
+                 scratch_block=100, fused_min_rows=16, fused_max_rows=256, embed=4096, final_norm=4096,
+                 unit_gain=4096, rope_cos=4096, rope_sin=4096, hidden=4096, layers=layers)
+        d.update(kw)
+        return _lib.RunnerDesc(**d)
+    h = C.c_void_p()
+    bad, unsup = _lib.CVH_ERR_INVALID_ARG, _lib.CVH_ERR_UNSUPPORTED
+    assert lib.cvh_runner_create(None, C.byref(h)) == bad
+    assert lib.cvh_runner_create(C.byref(desc(embed=None)), C.byref(h)) == bad
+    assert lib.cvh_runner_create(C.byref(desc(max_batch=257)), C.byref(h)) == bad
+    assert lib.cvh_runner_create(C.byref(desc(n_heads=12)), C.byref(h)) == bad          # 12 % 8 != 0
+    assert lib.cvh_runner_create(C.byref(desc(intermediate=3000)), C.byref(h)) == unsup  # K % 128 != 0
+    assert lib.cvh_runner_create(C.byref(desc(dim=2048)), C.byref(h)) == unsup           # fused rows <= 1024
+    layers[1].w_qkv_folded = None
+    assert lib.cvh_runner_create(C.byref(desc()), C.byref(h)) == bad                      # fused weights missing
+    assert h.value is None
+    for fn, args in ((lib.cvh_runner_forward, (4, 0, None)), (lib.cvh_runner_capture, (4, 0)),
+                     (lib.cvh_runner_replay, (4, 0, None)), (lib.cvh_runner_destroy, ())):
+        assert fn(C.c_void_p(4096), *args) == bad
