@@ -1690,7 +1690,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     // shared-prefix launches (plan_shared and the _shared launches) use the larger layout; units run
     // where the MFMA unit path exists (head_dim 128, GQA 2, one row group per token)
     const bool shared = (phase & kPhaseShared) || shared_blocks != nullptr;
-    const bool units_on = shared && head_dim == 128 && rep_v == 2 && n_kv_heads == wpg;
+    // (the plan's grouping compares token pairs: up to 2048 query tokens, far above a decode batch)
+    const bool units_on = shared && head_dim == 128 && rep_v == 2 && n_kv_heads == wpg && num_tokens <= 2048;
     const Workspace wl = ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G, shared);
     if (workspace == nullptr || workspace_bytes < wl.total) return CVH_ERR_WORKSPACE;
     char* wsb = static_cast<char*>(workspace);
