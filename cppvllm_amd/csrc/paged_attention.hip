@@ -19,8 +19,8 @@
 //     the pieces of cut rows.
 //   * shared-prefix units (planned shared launches): the plan groups tokens whose block tables
 //     start with the same shared blocks (prefix-cache hits) and appends one row per unit of up to
-//     8 such tokens after the real rows; a unit's tiles are the group's shared keys, multiplied on
-//     matrix cores against the 16 query columns of its tokens (8 tokens x 2 query heads), so the
+//     16 / REP such tokens after the real rows; a unit's tiles are the group's shared keys, multiplied
+//     on matrix cores against the 16 query columns of its tokens (16 / REP tokens x REP heads), so the
 //     prefix is read once per unit instead of once per token. Members' own rows start after the
 //     shared keys; member rows and units always end as partials, which the merge combines.
 //
@@ -251,7 +251,7 @@ struct PlanRec {
     int pad[3];
 };
 
-constexpr int kUnitTokens = 8;             // member tokens per shared-prefix unit (16 MFMA columns at GQA 2)
+constexpr int kUnitTokens = 16;            // most member tokens of a shared-prefix unit (16 MFMA columns, GQA 1)
 struct UnitRec {
     int seq;                               // block-table row of the group's first member
     int keys;                              // shared keys (a multiple of the block size, or a whole context)
@@ -266,10 +266,10 @@ struct Params {
     int2* plan_tok;          // [T] (kv_len, block-table row) per token, written by the plan kernel
     int* shared_tok;         // [T] keys of token t in blocks shared with another sequence (plan kernel)
     const int32_t* shared_blocks;   // [table rows] leading shared blocks per row (plan input), or null
-    // Shared-prefix units (planned shared launches at head_dim 128, GQA 2, one row group per token):
+    // Shared-prefix units (planned shared launches at head_dim 128, one row group per token):
     // sequences whose block tables start with the same shared blocks are grouped; each group's
-    // shared keys are read once per unit of up to 8 member tokens (16 MFMA columns: 8 tokens x 2
-    // query heads per kv head), and each member's own row starts after them.
+    // shared keys are read once per unit of up to unit_tokens member tokens (16 MFMA columns:
+    // unit_tokens tokens x the query heads of one kv head), and each member's own row starts after them.
     UnitRec* units;          // [max_units] unit records (plan output)
     int* unit_count;         // [1] number of units (plan output)
     int2* tok_unit;          // [T] (unit, column) of a member token, (-1, 0) otherwise
@@ -280,6 +280,7 @@ struct Params {
     float* psh_acc;          // [G][2][WPG][16][HD] partials of units cut by a range boundary
     float* psh_ml;           // [G][2][WPG][16][2]
     int max_units;
+    int unit_tokens;         // member tokens per unit: 16 MFMA columns / query heads per kv head
     float* part_acc;         // [G][2][WPG][REP][HD]
     float* part_ml;          // [G][2][WPG][REP][2]
     int* prefix_out;         // [rows + 1] row tile prefix, written by workgroup 0 for the merge
@@ -392,6 +393,7 @@ __device__ int build_units(const Params& p, int2* tok) {
     const int T = p.num_tokens, tid = threadIdx.x, nth = blockDim.x;
     const int log2_bs = p.log2_bs;
     const int64_t W = p.table_width;
+    const int ut = p.unit_tokens;
     if (tid == 0) n_units = 0;
     for (int i = tid; i < p.max_units; i += nth) p.units[i].n = 0;
     auto keys_of = [&](int t) -> int {
@@ -446,12 +448,12 @@ __device__ int build_units(const Params& p, int2* tok) {
         if (lead < 0 || p.shared_tok[lead] < 2) continue;
         int base = 0;
         for (int u = 0; u < lead; ++u)
-            if (p.tok_unit[u].x == u && p.shared_tok[u] >= 2) base += (p.shared_tok[u] + kUnitTokens - 1) / kUnitTokens;
+            if (p.tok_unit[u].x == u && p.shared_tok[u] >= 2) base += (p.shared_tok[u] + ut - 1) / ut;
         const int j = p.tok_unit[t].y;
-        my_unit[k & 7] = base + j / kUnitTokens;
-        my_col[k & 7] = j % kUnitTokens;
+        my_unit[k & 7] = base + j / ut;
+        my_col[k & 7] = j % ut;
         my_keys[k & 7] = keys_of(t);
-        if (lead == t) atomicAdd(&n_units, (p.shared_tok[t] + kUnitTokens - 1) / kUnitTokens);
+        if (lead == t) atomicAdd(&n_units, (p.shared_tok[t] + ut - 1) / ut);
     }
     __syncthreads();
     k = 0;
@@ -531,8 +533,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     extern __shared__ int prefix[];
     const int wpg = p.wpg;
     const int hg_count = p.n_kv / wpg;
-    // shared-prefix units run on the MFMA path at head_dim 128 and GQA 2 (16 columns: 8 tokens x 2 heads)
-    constexpr bool UNITS = SHARED && HD == 128 && REP == 2;
+    // shared-prefix units run on the MFMA path at head_dim 128 (16 columns: 16 / REP tokens x REP heads)
+    constexpr bool UNITS = SHARED && HD == 128;
     const int rows_real = p.num_tokens * hg_count;
     const int rows = rows_real + ((UNITS && p.units != nullptr) ? ld_uniform(p.unit_count, 0) : 0);
     int2* tok = reinterpret_cast<int2*>(reinterpret_cast<char*>(prefix) + lds_tok_offset(rows_real + p.max_units));
@@ -1052,7 +1054,19 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             float Lr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) Lr[r] = __shfl(L, 4 * g4 + r, 64);   // heads of this lane's O rows
-            if (pc.lt == 0 && pc.le == pr1 - pr0) {
+            if (UNITS && pc.shared_keys > 0 && pc.lt == 0 && pc.le == pr1 - pr0) {
+                // a member row held whole: its partial joins the unit's in the merge
+                const int64_t base = (int64_t)pc.t * H + pc.g * REP;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int head = 4 * g4 + r;
+                    if (head >= REP) continue;
+                    float* pa = p.ptok_acc + (base + head) * HD + 8 * i16;
+                    *reinterpret_cast<float4*>(pa) = make_float4(om[0][r], om[1][r], om[2][r], om[3][r]);
+                    *reinterpret_cast<float4*>(pa + 4) = make_float4(om[4][r], om[5][r], om[6][r], om[7][r]);
+                }
+                if (g4 == 0 && i16 < REP) reinterpret_cast<float2*>(p.ptok_ml)[base + i16] = make_float2(mm, L);
+            } else if (pc.lt == 0 && pc.le == pr1 - pr0) {
                 const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? p.v_scale[0] : 1.f;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -1257,7 +1271,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     }
     if constexpr (UNITS) {
         // ---- shared-prefix units of the range: each wave multiplies its kv head's K/V tiles of the
-        // group's shared keys against 16 query columns (8 member tokens x 2 heads), one pass per unit
+        // group's shared keys against 16 query columns (16 / REP member tokens x REP heads), one pass per unit
         // instead of one per member; the tiles are read with the default cache policy so the other
         // units of the group find them in L2 / the last-level cache
         if (p.units != nullptr) {
@@ -1282,10 +1296,10 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 int tile = pc.lt;
                 mf_load(pol, pc, tile, TA, lookup(pc, tile), true);
                 mf_load(pol, pc, min(tile + 1, pc.le - 1), TB, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
-                {   // column c = 2 j + h: member j's query head 2 wi + h (zero past the unit's members)
-                    const int j = i16 >> 1, hh = i16 & 1;
+                {   // column c = REP j + h: member j's query head REP wi + h (zero past the unit's members)
+                    const int j = i16 / REP, hh = i16 % REP;
                     const int tj = j < n ? ur->tok[j] : 0;
-                    const uint16_t* src = p.q + ((int64_t)tj * H + 2 * wi + hh) * HD;
+                    const uint16_t* src = p.q + ((int64_t)tj * H + REP * wi + hh) * HD;
 #pragma unroll
                     for (int st = 0; st < 4; ++st) {
                         uint4 v = make_uint4(0u, 0u, 0u, 0u);
@@ -1408,7 +1422,7 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
             }
         }
         if (member) {                                // the unit's column of this head
-            const int wv = hh / rep, col = 2 * tu.y + hh % rep;
+            const int wv = hh / rep, col = rep * tu.y + hh % rep;
             if (v0 == v1) {
                 if (part == 0) {
                     const int64_t idx = (static_cast<int64_t>(tu.x) * wpg + wv) * 16 + col;
@@ -1574,10 +1588,12 @@ struct Workspace {
     int max_units;
 };
 size_t align256(size_t v) { return (v + 255) & ~size_t{255}; }
-int max_units_for(int64_t T) { return static_cast<int>(T / 2); }
+// groups have two or more tokens and units up to 16 / rep of them: at most T / 2 units (2 T / 3 at
+// two tokens per unit)
+int max_units_for(int64_t T, int rep) { return static_cast<int>(rep >= 8 ? (2 * T + 2) / 3 : (T + 1) / 2); }
 Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G, bool shared = false) {
     const int64_t hg = n_kv / waves_per_group(n_kv);
-    const int64_t rows = T * hg + (shared ? max_units_for(T) : 0);
+    const int64_t rows = T * hg + (shared ? max_units_for(T, n_heads / n_kv) : 0);
     const int64_t slots = static_cast<int64_t>(G) * 2 * (n_heads / hg);   // [G][2][WPG*REP]
     Workspace w;
     w.prefix_off = 0;
@@ -1587,7 +1603,7 @@ Workspace ws_layout(int64_t T, int n_heads, int n_kv, int HD, int G, bool shared
     w.shared_off = w.tok_off + align256(static_cast<size_t>(T) * sizeof(int2));
     w.plan_off = w.shared_off + align256(static_cast<size_t>(T) * sizeof(int));
     w.total = w.plan_off + align256(static_cast<size_t>(G) * sizeof(PlanRec));
-    w.max_units = shared ? max_units_for(T) : 0;
+    w.max_units = shared ? max_units_for(T, n_heads / n_kv) : 0;
     w.units_off = w.ucount_off = w.tok_unit_off = w.ptok_acc_off = w.ptok_ml_off = w.punit_acc_off = w.punit_ml_off =
             w.psh_acc_off = w.psh_ml_off = w.total;
     if (shared) {
@@ -1688,10 +1704,10 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
         return CVH_ERR_UNSUPPORTED;
     const int G = partitions ? partitions : auto_partitions(num_tokens, n_kv_heads, table_width, block_size);
     // shared-prefix launches (plan_shared and the _shared launches) use the larger layout; units run
-    // where the MFMA unit path exists (head_dim 128, GQA 2, one row group per token)
+    // where the MFMA unit path exists (head_dim 128, one row group per token)
     const bool shared = (phase & kPhaseShared) || shared_blocks != nullptr;
     // (the plan's grouping compares token pairs: up to 2048 query tokens, far above a decode batch)
-    const bool units_on = shared && head_dim == 128 && rep_v == 2 && n_kv_heads == wpg && num_tokens <= 2048;
+    const bool units_on = shared && head_dim == 128 && n_kv_heads == wpg && num_tokens <= 2048;
     const Workspace wl = ws_layout(num_tokens, n_heads, n_kv_heads, head_dim, G, shared);
     if (workspace == nullptr || workspace_bytes < wl.total) return CVH_ERR_WORKSPACE;
     char* wsb = static_cast<char*>(workspace);
@@ -1699,6 +1715,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     Params p{};
     p.out = static_cast<uint16_t*>(out);
     p.max_units = wl.max_units;
+    p.unit_tokens = 16 / rep_v;
     if (units_on) {
         p.units = reinterpret_cast<UnitRec*>(wsb + wl.units_off);
         p.unit_count = reinterpret_cast<int*>(wsb + wl.ucount_off);

@@ -59,8 +59,8 @@ def paged_attention_plan(block_tables, token_seq, token_kv_len, n_heads: int, n_
     """Build the per-step plan that ``paged_attention_fp8(..., planned=True)`` reads from `workspace`
     (once per batch layout, before the layers of a step). shared_blocks (int32, one per table row):
     leading blocks each row shares with other rows (prefix-cache hits): tokens whose rows share them
-    are grouped, and the shared launches read each group's shared K/V once per unit of up to 8
-    tokens (needs a workspace made with shared=True)."""
+    are grouped, and the shared launches read each group's shared K/V once per unit of up to
+    16 / (query heads per kv head) tokens at head_dim 128 (needs a workspace made with shared=True)."""
     T = token_seq.size(0)
     if T == 0:
         return

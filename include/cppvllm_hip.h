@@ -166,11 +166,11 @@ int cvh_paged_attention_plan(const int64_t* block_tables, int64_t table_width, c
  * manager's reference counts). Query tokens whose rows start with the same physical blocks (same
  * first block, same shared key count s = min(kv_len, shared_blocks * block_size), same first
  * ceil(s / block_size) table entries) form a group; a group of two or more is split in token order
- * into units of up to 8 tokens. The _planned_shared launches (same arguments as _planned) then read
- * each unit's shared K/V once for all its tokens (one matrix-core pass: 8 tokens x 2 query heads
- * per kv head as 16 MFMA columns) and each token's own tiles from key s on, and the merge combines
- * the two per token. Units run at head_dim 128 with 2 query heads per kv head, at most 8 kv heads
- * and at most 2048 query tokens; other launches, and tokens in no group, run as the plain plan. Results equal the plain
+ * into units of up to 16 / (query heads per kv head) tokens. The _planned_shared launches (same
+ * arguments as _planned) then read each unit's shared K/V once for all its tokens (one matrix-core
+ * pass: the unit's tokens x their query heads of one kv head as 16 MFMA columns) and each token's
+ * own tiles from key s on, and the merge combines the two per token. Units run at head_dim 128
+ * (GQA 1, 2, 4, 8: units of 16, 8, 4, 2 tokens), at most 8 kv heads and at most 2048 query tokens; other launches, and tokens in no group, run as the plain plan. Results equal the plain
  * launches within the attention tolerance (another summation order), and are bitwise reproducible.
  * Workspace: cvh_paged_attention_workspace_bytes_shared bytes (the plan, the _shared launches and
  * their merge phase use the same layout).

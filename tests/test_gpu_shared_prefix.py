@@ -3,7 +3,7 @@ launches) on the GPU, against the CPU oracle.
 
 Sequences whose block tables start with the same physical blocks (prefix-cache hits,
 engine/block_manager.cpp:80-116) are grouped by the plan; each group's shared keys are read once
-per unit of up to 8 member tokens (one matrix-core pass over 8 tokens x 2 query heads per kv head)
+per unit of up to 16 / GQA member tokens (one matrix-core pass over 16 query columns per kv head)
 and each member's own tiles start after them; the merge combines the two. The result must equal
 the oracle's attention over the whole context of every token (every row checked), be bitwise
 reproducible, and agree with the plain planned launch within the attention tolerance (another
@@ -56,7 +56,7 @@ def run_planned(b, shared: bool, partitions: int = 0, phases: bool = False):
     return bits(out)
 
 
-def grouped_batch(seed, BS, groups, singles, per_tensor=False, pad=True):
+def grouped_batch(seed, BS, groups, singles, per_tensor=False, pad=True, n_heads=16):
     """groups: list of (n_members, shared_blocks, [extra keys per member]); singles: context lengths
     of sequences that share nothing; one sequence reports shared blocks without a partner; a
     padding token (token_seq -1) at the end when pad."""
@@ -97,10 +97,10 @@ def grouped_batch(seed, BS, groups, singles, per_tensor=False, pad=True):
     tseq = order + ([-1] if pad else [])
     tlen = [rows[i][1] for i in order] + ([50] if pad else [])
     T = len(tseq)
-    q = torch.randn((T, 16, 128), generator=g).to(torch.bfloat16)
+    q = torch.randn((T, n_heads, 128), generator=g).to(torch.bfloat16)
     return {"q": q, "k_cache": kc, "v_cache": vc, "k_scale": ks, "v_scale": vs, "block_tables": table,
             "token_seq": torch.tensor(tseq, dtype=torch.int64), "token_kv_len": torch.tensor(tlen, dtype=torch.int64),
-            "shared_blocks": torch.tensor(shared_cnt, dtype=torch.int32), "block_size": BS, "n_heads": 16,
+            "shared_blocks": torch.tensor(shared_cnt, dtype=torch.int32), "block_size": BS, "n_heads": n_heads,
             "n_kv_heads": 8, "head_dim": 128, "scale": 1 / math.sqrt(128)}
 
 
@@ -141,11 +141,34 @@ def test_units_grouped_batch(orc, BS, per_tensor):
         assert_close_bf16(run_planned(d, True, partitions=parts), want, ulp_floor=True)
 
 
+@pytest.mark.parametrize("H", [8, 32, 64])
+def test_units_other_gqa(orc, H):
+    """GQA 1 / 4 / 8 at head_dim 128: units of 16 / 4 / 2 member tokens (16 matrix-core columns),
+    groups of 2 to 19 members, whole and cut units, split / merge phases."""
+    groups = [(2, 2, [40]), (3, 1, [7, 100, 0]), (8, 3, [1, 300, 17, 64]), (19, 1, [200, 5, 1000, 33, 0]),
+              (4, 2, [-7, 10])]
+    say(f"shared-prefix units at GQA {H // 8}: groups of 2/3/8/19/4 members")
+    b = grouped_batch(300 + H, 64, groups, singles=[90, 2000, 1], n_heads=H)
+    want = run_oracle(orc, b)
+    d = to_dev(b)
+    got = run_planned(d, True)
+    assert_close_bf16(got, want, ulp_floor=True)
+    assert not got[-1].any(), "the padding token's row must be zero"
+    assert np.array_equal(got, run_planned(d, True))
+    assert np.array_equal(got, run_planned(d, True, phases=True))
+    plain = run_planned(d, False)
+    ts = b["token_seq"].numpy()
+    shared_rows = np.nonzero((ts >= 0) & (b["shared_blocks"].numpy()[ts.clip(0)] > 0))[0]
+    assert not np.array_equal(got[shared_rows], plain[shared_rows]), "the units did not run"
+    for parts in (3, 64, 700):
+        assert_close_bf16(run_planned(d, True, partitions=parts), want, ulp_floor=True)
+
+
 def test_units_respect_head_layout_limits(orc):
-    """Shapes without the unit path (head_dim 64, GQA 1) accept the shared plan and run it as the
-    plain one, matching the oracle."""
-    say("shared plan on shapes without units (HD 64 GQA 2, HD 128 GQA 1)")
-    for HD, H in ((64, 16), (128, 8)):
+    """Shapes without the unit path (head_dim 64, kv heads in several row groups) accept the
+    shared plan and run it as the plain one, matching the oracle."""
+    say("shared plan on shapes without units (HD 64 GQA 2)")
+    for HD, H in ((64, 16),):
         b = grouped_batch(7 + HD + H, 256, [(4, 2, [30, 500])], singles=[300])
         g = torch.Generator().manual_seed(HD + H)
         b["n_heads"], b["head_dim"], b["scale"] = H, HD, 1 / math.sqrt(HD)
