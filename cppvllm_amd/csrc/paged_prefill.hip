@@ -19,8 +19,8 @@
 // PV step (the keys its S^T output holds).
 //
 // Work: a workgroup = (64 consecutive query tokens, one kv head), 4 waves of 16 tokens each
-// (REP query heads per token), walking the keys of the tokens' sequence in 32-key tiles. The 256
-// threads load each tile once for all four waves: K is converted to bf16 and V transposed to fp16
+// (REP query heads per token), walking the keys of the tokens' sequence in 64-key tiles (staged
+// as two 32-key load groups). The 256 threads load each tile once for all four waves: K is converted to bf16 and V transposed to fp16
 // (each thread loads a 4 key x 4 d byte block with dword loads, transposes it with v_perm_b32 and
 // converts it) into a double-buffered LDS tile, so one tile is multiplied while the next sits in
 // registers and the one after is in flight. Tokens of different sequences inside the 64 run as
@@ -40,13 +40,14 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kHD = 128;
 constexpr int kQTok = 16;          // query tokens per wave
-constexpr int kTile = 32;          // keys per tile
+constexpr int kTile = 64;          // keys per tile (multiplied between two synchronisations)
+constexpr int kSub = 32;           // keys per load group (a tile is staged as two)
 // LDS row strides chosen against bank conflicts (64 banks of 4 bytes):
-//  * V^T rows are 18 dwords (32 keys + 4 pad bf16), 8-byte aligned, so a lane's 16 fragment
+//  * V^T rows are 38 dwords (64 keys + 12 pad fp16), 8-byte aligned, so a lane's 32 fragment
 //    reads are ds_read_b64 at immediate offsets from one address (rows j*16 + i16 lie
-//    j * 1152 bytes apart); the 16 rows read together land on distinct even banks;
+//    j * 2432 bytes apart); the 16 rows read together land on distinct even banks;
 //  * K rows are 136 bf16 (272 bytes): the 16 rows read by one 16-byte load land 4 banks apart.
-constexpr int kVtStride = 36;      // bf16 per LDS row of V^T
+constexpr int kVtStride = 76;      // fp16 per LDS row of V^T
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kNegHuge = -1e30f;
 constexpr float kRescaleLog2 = 8.0f;   // tolerated staleness of the running max (log2 units)
@@ -103,7 +104,6 @@ __device__ __forceinline__ float sum_groups(float v) {
 constexpr int kWgTok = 4 * kQTok;  // query tokens per workgroup: 16 per wave
 constexpr int kKRow = kHD + 8;      // bf16 per LDS row of K (272 bytes: 16 rows of a read hit distinct banks)
 
-// One double-buffered K/V tile in LDS: K as bf16 rows, V transposed (V^T rows = d), scales.
 // A double-buffered K/V tile in LDS: K as bf16 rows, V transposed (V^T rows = d), scales.
 struct PrefillLds {
     uint16_t k[2][kTile][kKRow];
@@ -113,9 +113,9 @@ struct PrefillLds {
     int tkvl[kWgTok];
 };
 
-// The workgroup's share of one tile as loaded by thread tid (raw e4m3 and f32 scales):
-// K: key tid/8, bytes (tid%8)*16 .. +16;  V: keys 4*(tid/32) + e, bytes 4*(tid%32) .. +4;
-// scales: key tid/8. Every wave's keys lie in one half of the tile (wave w: keys 8w .. 8w+7),
+// The workgroup's share of one 32-key load group as loaded by thread tid (raw e4m3 and f32
+// scales): K: key tid/8, bytes (tid%8)*16 .. +16;  V: keys 4*(tid/32) + e, bytes 4*(tid%32) .. +4;
+// scales: key tid/8. Every wave's keys lie in one half of the group (wave w: keys 8w .. 8w+7),
 // so with 16-key blocks each wave still reads from a single block.
 struct TileRegs {
     uint4 k;
@@ -206,8 +206,8 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     const int64_t my_seq = smv[0].tseq[16 * w + i16];
     const int my_kvl = smv[0].tkvl[16 * w + i16];
     // this wave's keys: [8w, 8w + 8) of every tile; with 16-key blocks waves 2, 3 read the second block
-    const int khalf = (BS < kTile && w >= 2) ? 16 : 0;
-    const int khalf_span = BS < kTile ? 16 : kTile;
+    const int khalf = (BS < kSub && w >= 2) ? 16 : 0;
+    const int khalf_span = BS < kSub ? 16 : kSub;
     const uint32_t row_bytes32 = static_cast<uint32_t>(row_bytes);
     const uint32_t k_off = static_cast<uint32_t>((tid >> 3) - khalf) * row_bytes32 + kvh * kHD + (tid & 7) * 16;
     const uint32_t v_off = static_cast<uint32_t>(4 * (tid >> 5) - khalf) * row_bytes32 + kvh * kHD + (tid & 31) * 4;
@@ -292,9 +292,9 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
         };
         // registers -> LDS buffer: K converted to bf16, V transposed to fp16 (4x4 byte blocks with
         // v_perm_b32) and converted, scales
-        auto store_tile = [&](int buf, const TileRegs& r) {
+        auto store_tile = [&](int buf, int sub, const TileRegs& r) {
             {
-                const int key = tid >> 3, cc = tid & 7;
+                const int key = sub * kSub + (tid >> 3), cc = tid & 7;
                 const uint4 lo = make_uint4(pk_bf16<false>(r.k.x), pk_bf16<true>(r.k.x), pk_bf16<false>(r.k.y),
                                             pk_bf16<true>(r.k.y));
                 const uint4 hi = make_uint4(pk_bf16<false>(r.k.z), pk_bf16<true>(r.k.z), pk_bf16<false>(r.k.w),
@@ -315,20 +315,21 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                                         __builtin_amdgcn_perm(dd, b, 0x07060302u)};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.vt[buf][(c * 4 + e) * kVtStride + 4 * kg]);
+                    uint32_t* dst = reinterpret_cast<uint32_t*>(&sm.vt[buf][(c * 4 + e) * kVtStride + sub * kSub + 4 * kg]);
                     dst[0] = pk_f16<false>(tr[e]);
                     dst[1] = pk_f16<true>(tr[e]);
                 }
             }
             if ((tid & 7) == 0) {
-                sm.ks[buf][tid >> 3] = r.ks * scale_log2;
-                sm.vs[buf][tid >> 3] = r.vs;
+                sm.ks[buf][sub * kSub + (tid >> 3)] = r.ks * scale_log2;
+                sm.vs[buf][sub * kSub + (tid >> 3)] = r.vs;
             }
         };
+        // kb = 16-key row block of the tile (4), PV step h = keys 32h .. 32h + 31 (2)
         auto compute = [&](int buf, int kb0, bool masked) {
-            f32x4_t sc[2][REP];
+            f32x4_t sc[4][REP];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 4; ++kb) {
                 bf16x8_t ka[4];
 #pragma unroll
                 for (int st = 0; st < 4; ++st)
@@ -343,9 +344,9 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                     sc[kb][rb] = acc;
                 }
             }
-            float ksr[2][4], vsr[2][4];
+            float ksr[4][4], vsr[4][4];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 4; ++kb) {
                 const float4 a = *reinterpret_cast<const float4*>(&sm.ks[buf][kb * 16 + g * 4]);
                 const float4 b = *reinterpret_cast<const float4*>(&sm.vs[buf][kb * 16 + g * 4]);
                 ksr[kb][0] = a.x; ksr[kb][1] = a.y; ksr[kb][2] = a.z; ksr[kb][3] = a.w;
@@ -353,13 +354,15 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
             }
             // the tile's largest V scale (scales are >= 0; keys past a context read 0); a new
             // range exponent only when it leaves [2^-6, 2^7) x 2^e
-            // (each lane tests its own 8 keys; only when some lane is above the window, or none
+            // (each lane tests its own 16 keys; only when some lane is above the window, or none
             // reaches it, does the wave reduce the maximum and move e, kept within [-100, 120] so
             // that p' = exp2(s - m - e) <= 2^108 stays a finite fp32)
             const float e_old = ew;
             {
-                float vm = fmaxf(fmaxf(fmaxf(vsr[0][0], vsr[0][1]), fmaxf(vsr[0][2], vsr[0][3])),
-                                 fmaxf(fmaxf(vsr[1][0], vsr[1][1]), fmaxf(vsr[1][2], vsr[1][3])));
+                float vm = 0.f;
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+                    vm = fmaxf(vm, fmaxf(fmaxf(vsr[kb][0], vsr[kb][1]), fmaxf(vsr[kb][2], vsr[kb][3])));
                 const uint64_t above = __builtin_amdgcn_ballot_w64(vm >= win_hi);
                 const uint64_t inside = __builtin_amdgcn_ballot_w64(vm >= win_lo);
                 if (above != 0 || inside == 0) {
@@ -373,22 +376,23 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                     }
                 }
             }
+            uint32_t pp[REP][2][4];
 #pragma unroll
             for (int rb = 0; rb < REP; ++rb) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) sc[kb][rb][r] *= ksr[kb][r];
                 if (masked) {              // wave-uniform: only tiles reaching past a row's length
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
+                    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             if (kb0 + kb * 16 + g * 4 + r >= row_kvl) sc[kb][rb][r] = -INFINITY;
                 }
                 float mt = kNegHuge;
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) mt = fmaxf(mt, sc[kb][rb][r]);
                 mt = max_groups(mt);
@@ -400,46 +404,58 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                 m[rb] = mn0;
                 const float mn = mn0 + ew;                                   // offset max of this tile's p
                 float ps = 0.f;
-                uint32_t pp[4];
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                     for (int r = 0; r < 4; r += 2) {
                         const float p0 = __builtin_amdgcn_exp2f(sc[kb][rb][r] - mn);
                         const float p1 = __builtin_amdgcn_exp2f(sc[kb][rb][r + 1] - mn);
                         ps += p0 + p1;
-                        pp[kb * 2 + r / 2] = pack_f16x2(p0 * vsr[kb][r], p1 * vsr[kb][r + 1]);
+                        pp[rb][kb >> 1][(kb & 1) * 2 + r / 2] = pack_f16x2(p0 * vsr[kb][r], p1 * vsr[kb][r + 1]);
                     }
                 lsum[rb] = lsum[rb] * alpha + ps;
                 if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {     // wave-uniform: the max moved
 #pragma unroll
                     for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
                 }
-                const f16x8_t pop = __builtin_bit_cast(f16x8_t, pp);
+            }
+            // PV, one 32-key step at a time: its V^T fragments serve every head
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const uint32_t* v32 = reinterpret_cast<const uint32_t*>(&sm.vt[buf][(j * 16 + i16) * kVtStride + g * 4]);
+                    const uint32_t* v32 = reinterpret_cast<const uint32_t*>(
+                            &sm.vt[buf][(j * 16 + i16) * kVtStride + h * kSub + g * 4]);
                     const uint2 lo = *reinterpret_cast<const uint2*>(v32), hi = *reinterpret_cast<const uint2*>(v32 + 8);
                     const uint32_t va[4] = {lo.x, lo.y, hi.x, hi.y};
-                    o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, va), pop,
-                                                                      o[rb][j], 0, 0, 0);
+#pragma unroll
+                    for (int rb = 0; rb < REP; ++rb)
+                        o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, va),
+                                                                          __builtin_bit_cast(f16x8_t, pp[rb][h]),
+                                                                          o[rb][j], 0, 0, 0);
                 }
             }
         };
 
-        // two-stage pipeline: tile i is multiplied from LDS while tile i+1 sits in registers
-        // (stored to the other buffer after the multiply) and tile i+2's loads are in flight
-        TileRegs rg;
-        load_tile(kbeg, rg);
-        store_tile(0, rg);
-        load_tile(kbeg + kTile, rg);
+        // two-stage pipeline: tile i is multiplied from LDS while tile i+1 sits in registers (two
+        // load groups, stored to the other buffer after the multiply) and tile i+2's loads are in
+        // flight
+        TileRegs ra, rb2;
+        load_tile(kbeg, ra);
+        load_tile(kbeg + kSub, rb2);
+        store_tile(0, 0, ra);
+        store_tile(0, 1, rb2);
+        load_tile(kbeg + kTile, ra);
+        load_tile(kbeg + kTile + kSub, rb2);
         tile_barrier();
         for (int i = 0, kb0 = kbeg; i < n_iter; ++i, kb0 += kTile) {
             const int buf = i & 1;
             if (kb0 < kend && kb0 < wave_kmax) compute(buf, kb0, kb0 + kTile > wave_kmin);
             if (kb0 + kTile < kend) {
-                store_tile(buf ^ 1, rg);
-                load_tile(kb0 + 2 * kTile, rg);
+                store_tile(buf ^ 1, 0, ra);
+                store_tile(buf ^ 1, 1, rb2);
+                load_tile(kb0 + 2 * kTile, ra);
+                load_tile(kb0 + 2 * kTile + kSub, rb2);
             }
             tile_barrier();
         }
@@ -563,7 +579,7 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(const int64_
         }
         if (gi < groups && (tid & 15) == 0) {
             kmax = min(kmax, max_keys);
-            const int c = static_cast<int>(min<int64_t>((kmax + kTile - 1) / kTile, kCostBuckets - 1));
+            const int c = static_cast<int>(min<int64_t>((kmax + kSub - 1) / kSub, kCostBuckets - 1));
             cost[gi] = c;
             atomicAdd(&hist[c], 1);
         }
