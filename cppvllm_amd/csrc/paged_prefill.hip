@@ -15,8 +15,9 @@
 // causal mask and its output accumulators live in the same lanes with no cross-lane shuffles
 // except the 4-way max/sum over lane groups. The contraction index order inside an MFMA is
 // free as long as A and B agree: lane group g = lane / 16 supplies d in
-// {c*64 + g*16 + h*8 + 0..7} for step s = 2c + h, and keys {g*4 + 0..3, 16 + g*4 + 0..3} for the
-// PV step (the keys its S^T output holds).
+// {c*64 + g*16 + h*8 + 0..7} for step s = 2c + h, and the 8 contiguous keys {8g + 0..7} of a
+// 32-key PV step (the score MFMAs take their K rows in the matching order, so these are the keys
+// the lane's S^T outputs hold and its V^T fragment is one 16-byte LDS read).
 //
 // Work: a workgroup = (64 consecutive query tokens, one kv head), 4 waves of 16 tokens each
 // (REP query heads per token), walking the keys of the tokens' sequence in 64-key tiles (staged
@@ -43,11 +44,11 @@ constexpr int kQTok = 16;          // query tokens per wave
 constexpr int kTile = 64;          // keys per tile (multiplied between two synchronisations)
 constexpr int kSub = 32;           // keys per load group (a tile is staged as two)
 // LDS row strides chosen against bank conflicts (64 banks of 4 bytes):
-//  * V^T rows are 38 dwords (64 keys + 12 pad fp16), 8-byte aligned, so a lane's 32 fragment
-//    reads are ds_read_b64 at immediate offsets from one address (rows j*16 + i16 lie
-//    j * 2432 bytes apart); the 16 rows read together land on distinct even banks;
+//  * V^T rows are 36 dwords (64 keys + 8 pad fp16), 16-byte aligned, so a lane's 16 fragment
+//    reads are ds_read_b128 at immediate offsets from one address (rows j*16 + i16 lie
+//    j * 2304 bytes apart); the 16 rows read by a quarter-wave land 4 banks apart;
 //  * K rows are 136 bf16 (272 bytes): the 16 rows read by one 16-byte load land 4 banks apart.
-constexpr int kVtStride = 76;      // fp16 per LDS row of V^T
+constexpr int kVtStride = 72;      // fp16 per LDS row of V^T
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr float kNegHuge = -1e30f;
 constexpr float kRescaleLog2 = 8.0f;   // tolerated staleness of the running max (log2 units)
@@ -210,7 +211,16 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
     const int khalf_span = BS < kSub ? 16 : kSub;
     const uint32_t row_bytes32 = static_cast<uint32_t>(row_bytes);
     const uint32_t k_off = static_cast<uint32_t>((tid >> 3) - khalf) * row_bytes32 + kvh * kHD + (tid & 7) * 16;
-    const uint32_t v_off = static_cast<uint32_t>(4 * (tid >> 5) - khalf) * row_bytes32 + kvh * kHD + (tid & 31) * 4;
+    // V: this thread's 4-key group (vkg) and 4-byte d block (vdc); a wave covers 16 keys (one block
+    // at 16-key blocks) x 64 d, a half-wave 4 key groups x 8 d blocks, so the V^T stores of a
+    // half-wave cover 32 rows (2-way bank conflicts at most)
+    const int vkg = (lane & 3) + 4 * (w >> 1), vdc = (lane >> 2) + 16 * (w & 1);
+    const uint32_t v_off = static_cast<uint32_t>(4 * vkg - khalf) * row_bytes32 + kvh * kHD + vdc * 4;
+    // K row position in LDS: key 32a + 8q + 4b + r of a tile sits at row 16(2a + b) + 4q + r, so the
+    // score rows of block kb (lane group g, element r) are keys 32(kb/2) + 8g + 4(kb%2) + r and each
+    // lane group's eight PV keys of a 32-key step are contiguous in V^T
+    const int kk = tid >> 3;
+    const int k_pos = 16 * ((kk >> 2) & 1) + 4 * (kk >> 3) + (kk & 3);
     const uint32_t s_off = static_cast<uint32_t>((tid >> 3) - khalf) * 4u;
     // The 4 waves sharing a tile buffer synchronise per tile. With two halves this is a counter in
     // LDS per half instead of the workgroup barrier, so the halves run their own tile counts and
@@ -294,7 +304,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
         // v_perm_b32) and converted, scales
         auto store_tile = [&](int buf, int sub, const TileRegs& r) {
             {
-                const int key = sub * kSub + (tid >> 3), cc = tid & 7;
+                const int key = 2 * 16 * sub + k_pos, cc = tid & 7;
                 const uint4 lo = make_uint4(pk_bf16<false>(r.k.x), pk_bf16<true>(r.k.x), pk_bf16<false>(r.k.y),
                                             pk_bf16<true>(r.k.y));
                 const uint4 hi = make_uint4(pk_bf16<false>(r.k.z), pk_bf16<true>(r.k.z), pk_bf16<false>(r.k.w),
@@ -303,7 +313,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                 *reinterpret_cast<uint4*>(&sm.k[buf][key][cc * 16 + 8]) = hi;
             }
             {
-                const int kg = tid >> 5, c = tid & 31;
+                const int kg = vkg, c = vdc;
                 const uint32_t w0 = r.v[0], w1 = r.v[1], w2 = r.v[2], w3 = r.v[3];
                 const uint32_t a = __builtin_amdgcn_perm(w1, w0, 0x05010400u);   // w0b0 w1b0 w0b1 w1b1
                 const uint32_t b = __builtin_amdgcn_perm(w1, w0, 0x07030602u);   // w0b2 w1b2 w0b3 w1b3
@@ -321,8 +331,8 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                 }
             }
             if ((tid & 7) == 0) {
-                sm.ks[buf][sub * kSub + (tid >> 3)] = r.ks * scale_log2;
-                sm.vs[buf][sub * kSub + (tid >> 3)] = r.vs;
+                sm.ks[buf][2 * 16 * sub + k_pos] = r.ks * scale_log2;
+                sm.vs[buf][2 * 16 * sub + k_pos] = r.vs;
             }
         };
         // kb = 16-key row block of the tile (4), PV step h = keys 32h .. 32h + 31 (2)
@@ -388,7 +398,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            if (kb0 + kb * 16 + g * 4 + r >= row_kvl) sc[kb][rb][r] = -INFINITY;
+                            if (kb0 + (kb >> 1) * 32 + g * 8 + (kb & 1) * 4 + r >= row_kvl) sc[kb][rb][r] = -INFINITY;
                 }
                 float mt = kNegHuge;
 #pragma unroll
@@ -424,10 +434,7 @@ __global__ __launch_bounds__(KSPLIT ? 512 : 256, KSPLIT ? 1 : 2) void paged_pref
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const uint32_t* v32 = reinterpret_cast<const uint32_t*>(
-                            &sm.vt[buf][(j * 16 + i16) * kVtStride + h * kSub + g * 4]);
-                    const uint2 lo = *reinterpret_cast<const uint2*>(v32), hi = *reinterpret_cast<const uint2*>(v32 + 8);
-                    const uint32_t va[4] = {lo.x, lo.y, hi.x, hi.y};
+                    const uint4 va = *reinterpret_cast<const uint4*>(&sm.vt[buf][(j * 16 + i16) * kVtStride + h * kSub + g * 8]);
 #pragma unroll
                     for (int rb = 0; rb < REP; ++rb)
                         o[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, va),
