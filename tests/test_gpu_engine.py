@@ -400,16 +400,31 @@ def test_prefix_cache_sharing_uses_shared_graphs():
     assert outs[0][0] == outs[1][0]
     assert [o[0] for o in outs[0]] == [o[0] for o in outs[1]]
 
+def _teacher_forced_gaps(m, prompt, out):
+    """Run prompt + out through the torch fp32 restatement (ref_forward) in one pass and return,
+    for every generated token, how far its logit lies below that position's largest logit."""
+    toks = torch.tensor(prompt + out, device=DEV)
+    x = ref_forward(m, toks, torch.arange(len(toks), device=DEV))
+    lg = x[len(prompt) - 1:len(prompt) - 1 + len(out)].to(torch.bfloat16).float() @ m.embed.float().T
+    chosen = lg[torch.arange(len(out), device=DEV), torch.tensor(out, device=DEV)]
+    return lg.max(-1).values - chosen
+
+
 def test_preemption_by_recompute_keeps_outputs():
     """A 16-block pool (256 cache slots) for six requests that need ~650: running sequences are
     preempted when blocks run out (engine/scheduler.cpp: the newest running sequence is evicted and
     later recomputed as a prefill of its whole context). Every request still produces its token
-    count and the pool is whole again at the end. Tokens are compared with a run whose pool never
-    fills: the batches differ after the preemption (other row counts pick other GEMM tilings and
-    attention partitions, so bf16 roundings differ), so exact equality is not a property of the
-    engine; with peaked logits (weights N(0, 0.5)) every request agrees on its first 16 tokens and
-    at least five of six agree on all of them (a recompute that wrote wrong K/V would diverge at
-    once)."""
+    count and the pool is whole again at the end.
+    Tokens: every generated token of both this run and a run whose pool never fills is checked by
+    teacher forcing against the torch fp32 restatement (the prompt plus the run's own tokens in one
+    pass): each must lie within GAP logits of the restatement's largest logit at its position, and at
+    most 10% may differ from that argmax. The weights (N(0, 0.5)) give logits with a standard
+    deviation of ~16 (top-1/top-2 margins ~3 at the median), the engine's bf16 roundings move them by
+    well under 1, while a recompute that wrote wrong K/V (positions, slots, scales) would pick tokens
+    tens of logits below the maximum. The two runs need not agree token for token: their batches
+    differ after the preemption (other row counts pick other GEMM tilings and attention partitions,
+    so bf16 roundings differ), so where they first diverge both tokens must be near-ties there."""
+    GAP = 2.0
     say("engine: preemption by recompute with a 16-block pool")
     g = torch.Generator().manual_seed(31)
     lens, outs_n = (40, 70, 33, 90, 25, 60), (60, 40, 80, 30, 70, 50)
@@ -423,5 +438,15 @@ def test_preemption_by_recompute_keeps_outputs():
     big = _engine(max_num_seqs=6, blocks=256, std=0.5)
     want = big.generate(prompts, params)
     assert big.stats().preemptions == 0
-    assert all(a[:16] == b[:16] for a, b in zip(got, want))
-    assert sum(a == b for a, b in zip(got, want)) >= 5
+    m = small.model
+    for i, (p, a, b) in enumerate(zip(prompts, got, want)):
+        for name, out in (("preempted", a), ("unpreempted", b)):
+            gap = _teacher_forced_gaps(m, p, out)
+            off = int((gap > 0).sum())
+            say(f"  request {i} {name}: max gap {gap.max().item():.3f}, {off} of {len(out)} off the argmax")
+            assert gap.max().item() <= GAP and off <= len(out) // 10
+        d = next((k for k in range(len(a)) if a[k] != b[k]), None)
+        if d is not None:                  # a near-tie under the restatement where the runs part
+            gap = _teacher_forced_gaps(m, p + a[:d], [a[d]]).item(), _teacher_forced_gaps(m, p + a[:d], [b[d]]).item()
+            say(f"  request {i}: runs part at token {d}, gaps {gap[0]:.3f} / {gap[1]:.3f}")
+            assert max(gap) <= GAP
