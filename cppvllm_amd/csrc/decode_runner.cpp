@@ -286,6 +286,8 @@ extern "C" int cvh_runner_forward(cvh_runner* r, int batch, int shared, cvh_stre
 extern "C" int cvh_runner_capture(cvh_runner* r, int batch, int shared) {
     if (!live(r) || batch <= 0 || batch > r->d.max_batch) return CVH_ERR_INVALID_ARG;
     hipStream_t s = r->capture_stream;
+    // the runner's stream does not wait on the caller's: let a preceding stage (on any stream) land
+    CVR_CHECK(hip_ok(hipDeviceSynchronize()));
     // one eager run first: kernels that opt in to large LDS set their attributes outside the capture
     CVR_CHECK(r->forward(batch, shared != 0, s));
     CVR_CHECK(hip_ok(hipStreamSynchronize(s)));

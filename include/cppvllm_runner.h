@@ -89,7 +89,10 @@ int cvh_runner_stage(cvh_runner* r, int slot, int64_t rows, int batch, const int
 /* The decode forward of the staged batch, launched eagerly on `stream`; writes desc.hidden. shared:
  * the attention plan marks each row's shared blocks (cvh_paged_attention_plan_shared). */
 int cvh_runner_forward(cvh_runner* r, int batch, int shared, cvh_stream_t stream);
-/* Capture the same forward into a HIP graph for (batch, shared) (replaces an earlier capture). */
+/* Capture the same forward into a HIP graph for (batch, shared) (replaces an earlier capture). It
+ * first waits for all device work, then runs the forward once eagerly on the runner's own stream
+ * (like cvh_runner_forward it writes the staged rows' K/V slots and desc.hidden): stage idle rows
+ * (rows = 0, which point at the scratch block) before capturing. Not for use during serving. */
 int cvh_runner_capture(cvh_runner* r, int batch, int shared);
 /* Replay the captured graph of (batch, shared) on `stream`; CVH_ERR_INVALID_ARG if none. */
 int cvh_runner_replay(cvh_runner* r, int batch, int shared, cvh_stream_t stream);
