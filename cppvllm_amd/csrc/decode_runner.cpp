@@ -249,6 +249,10 @@ extern "C" int cvh_runner_stage(cvh_runner* r, int slot, int64_t rows, int batch
     if (!live(r) || slot < 0 || slot > 1 || rows < 0 || batch <= 0 || batch > r->d.max_batch || rows > batch ||
         (rows > 0 && (tokens == nullptr || positions == nullptr || tables == nullptr || tables_width <= 0)))
         return CVH_ERR_INVALID_ARG;
+    // a position past the runner's table width would be clamped by the kernels, not attended
+    const int64_t max_pos = r->d.table_width * r->d.block_size;
+    for (int64_t i = 0; i < rows; ++i)
+        if (positions[i] < 0 || positions[i] >= max_pos) return CVH_ERR_INVALID_ARG;
     bool need_feed = false;
     if (feed != nullptr)
         for (int64_t i = 0; i < rows && !need_feed; ++i) need_feed = feed[i] >= 0;

@@ -79,7 +79,8 @@ int cvh_runner_destroy(cvh_runner* r);
 /* Stage `rows` decode rows padded to `batch` (rows <= batch <= max_batch) through pinned slot
  * `slot` (0 or 1: a slot is rewritten only after the step that used it has completed): host
  * tokens [rows], positions [rows], tables [rows][tables_width] (-1 padded; columns beyond the
- * runner's table_width are dropped), optional feed [rows] (>= 0: take the token from
+ * runner's table_width are dropped; a position outside [0, table_width * block_size) is
+ * rejected with CVH_ERR_INVALID_ARG), optional feed [rows] (>= 0: take the token from
  * prev_sampled[feed[i]], the device samples of the previous step; cvh_feed_tokens), optional
  * shared_blocks [rows] (leading blocks each row shares with other rows; used by shared forwards).
  * One host-to-device copy on `stream`. */

@@ -450,3 +450,22 @@ def test_preemption_by_recompute_keeps_outputs():
             gap = _teacher_forced_gaps(m, p + a[:d], [a[d]]).item(), _teacher_forced_gaps(m, p + a[:d], [b[d]]).item()
             say(f"  request {i}: runs part at token {d}, gaps {gap[0]:.3f} / {gap[1]:.3f}")
             assert max(gap) <= GAP
+
+
+def test_runner_stage_rejects_positions_past_the_table():
+    """cvh_runner_stage accepts the last position the runner's table width covers and rejects one
+    past it (the kernels would clamp the context instead of attending it) and a negative one."""
+    from cppvllm_amd import _lib
+    say("native runner: staged positions checked against the table width")
+    eng = _engine(blocks=64)
+    r = eng.runner
+    W, BS = r.graph_width, eng.cfg.block_size
+    t = np.zeros(1, np.int64)
+    tab = np.zeros((1, W), np.int64)
+    stream = torch.cuda.current_stream().cuda_stream
+    for pos, want in ((W * BS - 1, 0), (W * BS, _lib.CVH_ERR_INVALID_ARG), (-1, _lib.CVH_ERR_INVALID_ARG)):
+        p = np.array([pos], np.int64)
+        rc = r._L.cvh_runner_stage(r._handle, 0, 1, 1, t.ctypes.data, p.ctypes.data, tab.ctypes.data, W, None, None,
+                                   None, stream)
+        assert rc == want, (pos, rc)
+    torch.cuda.synchronize()
