@@ -180,11 +180,12 @@ def test_units_respect_head_layout_limits(orc):
         assert_close_bf16(got, run_oracle(orc, b), ulp_floor=True)
 
 
-@pytest.mark.parametrize("seed", range(12))
-def test_units_random_groups(orc, seed):
+@pytest.mark.parametrize("seed,H", [(s, 16) for s in range(12)] + [(100 + s, h) for s in range(3) for h in (8, 32, 64)])
+def test_units_random_groups(orc, seed, H):
     """Seeded random grouped batches: 1-5 groups of 2-20 members sharing 1-6 blocks with 0-2000 own
     keys (or a context inside the prefix), 0-20 other sequences, block size 16-1024, either scale
-    mode, automatic or random partition counts: every row against the oracle, reproducible."""
+    mode, automatic or random partition counts, 8 / 16 / 32 / 64 query heads over 8 kv heads (units of
+    16 / 8 / 4 / 2 tokens): every row against the oracle, reproducible."""
     r = np.random.default_rng(500 + seed)
     BS = int(r.choice([16, 32, 64, 256, 1024]))
     groups = []
@@ -196,9 +197,9 @@ def test_units_random_groups(orc, seed):
     singles = [int(r.integers(1, 3000)) for _ in range(int(r.integers(0, 21)))]
     per_tensor = bool(r.integers(2))
     parts = 0 if r.random() < 0.5 else int(r.integers(1, 500))
-    say(f"random shared-prefix case seed={seed} BS={BS} groups={[(g[0], g[1]) for g in groups]} "
+    say(f"random shared-prefix case seed={seed} H={H} BS={BS} groups={[(g[0], g[1]) for g in groups]} "
         f"singles={len(singles)} per_tensor={per_tensor} parts={parts}")
-    b = grouped_batch(900 + seed, BS, groups, singles, per_tensor=per_tensor)
+    b = grouped_batch(900 + seed, BS, groups, singles, per_tensor=per_tensor, n_heads=H)
     want = run_oracle(orc, b)
     d = to_dev(b)
     got = run_planned(d, True, partitions=parts)
