@@ -63,6 +63,7 @@ constexpr size_t kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
 constexpr int kMaxQRows = 8;
 constexpr int kPreQRows = 4;               // q rows a planned launch fetches ahead of its first tiles
+constexpr int kDeferMinTiles = 16;          // ranges this long hold their first cut piece's partial (MFMA path)
 constexpr int kResidentWaves = 2048;       // MI355X: 256 CUs x 4 SIMDs x 2 waves (<= 256 VGPRs each)
 
 // ---- buffer loads ------------------------------------------------------------------------------
@@ -525,7 +526,10 @@ struct Piece {
     int64_t seq;   // block-table row of token t
 };
 
-template <int HD, int REP, int SM, bool ONE_BLOCK, bool PLANNED, bool SHARED = false>
+// DEFER (MFMA path, full 8-kv-head row groups): the range's first cut piece is stored after the
+// range's tile stream (see `deferred` below); a separate instantiation because the held partial's
+// registers slow the short ranges of the one-kv-head shares down.
+template <int HD, int REP, int SM, bool ONE_BLOCK, bool PLANNED, bool SHARED = false, bool DEFER = false>
 __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     using V = KvVec<HD>;
     using VT = typename V::T;
@@ -566,6 +570,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     const int bs_mask = (1 << log2_bs) - 1;
 
     constexpr bool MF = REP >= 4;                   // GQA 4 / 8: score and PV products on MFMA
+    constexpr bool DEF = MF && DEFER;
     static_assert(!MF || HD == 128, "the MFMA path is laid out for head_dim 128");
     struct VTile {
         VT k[kSteps], v[kSteps];
@@ -870,6 +875,14 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     // MFMA path: softmax state of this lane's S^T column (one head), O rows of heads 4g..4g+3
     float mm = kMinusHuge, lm = 0.f;
     f32x4_t om[(MF || UNITS) ? 8 : 1];                         // [j]: d = 8*i16 + j, rows = heads 4g..4g+3
+    // MFMA path: the partial of the range's first piece when a boundary cuts it (slot 0), held in
+    // registers until the range's tile stream has ended. A store issued inside the stream would be
+    // waited for by the next tile's loads (one in-order vector-memory counter), and its write
+    // acknowledgement queues behind the saturating K/V reads. Short ranges store at once: there
+    // the deferred store would sit in the launch's tail instead.
+    f32x4_t dom[DEF ? 8 : 1];
+    float dmm = 0.f, dL = 0.f;
+    bool deferred = false;
     auto reset = [&]() {
         if constexpr (MF) {
             mm = kMinusHuge;
@@ -1079,6 +1092,12 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                                                               pack_bf16x2_rne(om[4][r] * f, om[5][r] * f),
                                                               pack_bf16x2_rne(om[6][r] * f, om[7][r] * f));
                 }
+            } else if (DEF && pr0 <= u0 && u1 - u0 >= kDeferMinTiles) {   // slot 0 of a long range: stored later
+#pragma unroll
+                for (int j = 0; j < (DEF ? 8 : 1); ++j) dom[j] = om[j];
+                dmm = mm;
+                dL = L;
+                deferred = true;
             } else {
                 const int slot = (pr0 <= u0) ? 0 : 1;
                 const int64_t base = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wi) * REP;
@@ -1268,6 +1287,20 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
         }
         rb = rlim;
         preQ = false;
+    }
+    if constexpr (DEF) {
+        if (deferred) {                    // the range's first cut piece, slot 0
+            const int64_t base = (static_cast<int64_t>(w) * 2 * wpg + wi) * REP;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int head = 4 * g4 + r;
+                if (head >= REP) continue;
+                float* pa = p.part_acc + (base + head) * HD + 8 * i16;
+                *reinterpret_cast<float4*>(pa) = make_float4(dom[0][r], dom[1][r], dom[2][r], dom[3][r]);
+                *reinterpret_cast<float4*>(pa + 4) = make_float4(dom[4][r], dom[5][r], dom[6][r], dom[7][r]);
+            }
+            if (g4 == 0 && i16 < REP) reinterpret_cast<float2*>(p.part_ml)[base + i16] = make_float2(dmm, dL);
+        }
     }
     if constexpr (UNITS) {
         // ---- shared-prefix units of the range: each wave multiplies its kv head's K/V tiles of the
@@ -1638,6 +1671,15 @@ void launch_with_lds(K kernel, int G, int threads, size_t lds, hipStream_t s, co
 // planned: 0 = derive the layout, 1 = read the plan, 2 = read the plan and its shared-prefix keys
 template <int HD, int REP, int SM, bool PLANNED, bool SHARED>
 void launch_decode_p(int G, int threads, size_t lds, hipStream_t s, const Params& p, bool one_block) {
+    if constexpr (REP >= 4) {
+        if (p.wpg == 8 && p.pack == 1) {      // full row groups: hold the first cut piece (DEFER)
+            if (one_block)
+                launch_with_lds(paged_decode_kernel<HD, REP, SM, true, PLANNED, SHARED, true>, G, threads, lds, s, p);
+            else
+                launch_with_lds(paged_decode_kernel<HD, REP, SM, false, PLANNED, SHARED, true>, G, threads, lds, s, p);
+            return;
+        }
+    }
     if (one_block)
         launch_with_lds(paged_decode_kernel<HD, REP, SM, true, PLANNED, SHARED>, G, threads, lds, s, p);
     else
