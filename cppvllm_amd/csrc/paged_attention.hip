@@ -1373,12 +1373,11 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 
 // Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One workgroup
 // per row (token, kv-head group): it recomputes, from the prefix the decode kernel stored, which
-// workgroups covered the row (wave-uniform scalar arithmetic) and exits if one did. The workgroup
-// is two halves with one thread per (query head, 4 dims) of the row each (wpg * rep * HD / 4 <=
-// 512 for every supported shape: wpg <= 8, rep <= 2 after the virtual-head split, HD <= 128);
-// half p folds pieces w0 + p, w0 + p + 2, ... online, then half 1 hands its (M, L, A) to half 0
-// through LDS, which combines the two, so a row's chain of dependent piece loads is half as long
-// (small batches cut a row into up to 8 pieces).
+// workgroups covered the row (wave-uniform scalar arithmetic) and exits if one did. One thread
+// per (query head, 4 dims) of the row (wpg * rep * HD / 4 <= 512 for every supported shape:
+// wpg <= 8, rep <= 2 after the virtual-head split, HD <= 128) folds the row's pieces online,
+// w0, w0 + 2, ... into one accumulator and w0 + 1, w0 + 3, ... into another, and combines the two
+// (small batches cut a row into up to 8 pieces; their loads go out four at a time).
 // Shared-prefix inputs of the merge (null when the launch has no units).
 struct MergeUnits {
     const int* unit_count;
@@ -1392,7 +1391,7 @@ struct MergeUnits {
 };
 
 template <int HD, int SM>
-__global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
+__global__ __launch_bounds__(512) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
                                                           const float* __restrict__ part_ml,
                                                           const int* __restrict__ prefix,
                                                           const float* __restrict__ v_scale, int num_tokens, int n_kv,
@@ -1412,83 +1411,103 @@ __global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict
     const bool member = tu.x >= 0;
     if (!member && pr1 == pr0) return;
     // workgroup holding tile u: the largest w with w*U/G <= u
-    auto owner = [&](int64_t u) { return static_cast<int>(((u + 1) * G - 1) / U); };
+    // workgroup holding tile u: the largest w with w*U/G <= u; 32-bit division whenever U * G fits
+    // (the 64-bit one is a long scalar routine)
+    const bool narrow = (U + 1) * G <= 0xffffffffll;
+    auto owner = [&](int64_t u) {
+        return narrow ? static_cast<int>((static_cast<uint32_t>(u + 1) * static_cast<uint32_t>(G) - 1u) / static_cast<uint32_t>(U))
+                      : static_cast<int>(((u + 1) * G - 1) / U);
+    };
+    auto first_tile = [&](int w) -> int64_t {    // first tile of workgroup w's range
+        return narrow ? static_cast<int64_t>(static_cast<uint32_t>(w) * static_cast<uint32_t>(U) / static_cast<uint32_t>(G))
+                      : w * U / G;
+    };
     const int w0 = pr1 > pr0 ? owner(pr0) : 0, w1 = pr1 > pr0 ? owner(pr1 - 1) : -1;
     if (!member && w0 == w1) return;
     const int64_t q0 = member ? prefix[rows_real + tu.x] : 0, q1 = member ? prefix[rows_real + tu.x + 1] : 0;
     const int v0 = member ? owner(q0) : 0, v1 = member ? owner(q1 - 1) : -1;
     const float vfin = (SM == CVH_SCALE_PER_TENSOR) ? v_scale[0] : 1.f;
-    __shared__ float xs[6][512];
-    const int half = static_cast<int>(blockDim.x) / 2, part = static_cast<int>(threadIdx.x) >= half ? 1 : 0;
-    const int slices = heads_per_row * TPH;          // a multiple of half (half = min(512, slices))
-    for (int base = 0; base < slices; base += half) {
-        const int ti = static_cast<int>(threadIdx.x) - part * half;
-        const int hh = (base + ti) / TPH;
-        const int d0 = ((base + ti) % TPH) * 4;
-        float M = kMinusHuge, L = 0.f;
-        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-        auto fold = [&](float2 ml, const float* src) {
-            const float4 a = *reinterpret_cast<const float4*>(src);
-            const float Mn = fmaxf(M, ml.x);
-            const float co = exp2f(M - Mn), cn = exp2f(ml.x - Mn);
-            L = L * co + ml.y * cn;
-            A.x = A.x * co + a.x * cn;
-            A.y = A.y * co + a.y * cn;
-            A.z = A.z * co + a.z * cn;
-            A.w = A.w * co + a.w * cn;
-            M = Mn;
-        };
+    // every thread owns slices (head, 4 dims) of the row; the pieces are folded into two
+    // accumulators, even and odd positions from the range's first piece, which are combined at the
+    // end. The loads of four consecutive pieces are issued together (indices of absent pieces
+    // clamped to the first one, their folds skipped), so a row's piece loads are not one dependent
+    // chain.
+    struct Acc {
+        float M, L;
+        float4 A;
+    };
+    auto fold = [](Acc& c, float2 ml, float4 a) {
+        const float Mn = fmaxf(c.M, ml.x);
+        const float co = exp2f(c.M - Mn), cn = exp2f(ml.x - Mn);
+        c.L = c.L * co + ml.y * cn;
+        c.A.x = c.A.x * co + a.x * cn;
+        c.A.y = c.A.y * co + a.y * cn;
+        c.A.z = c.A.z * co + a.z * cn;
+        c.A.w = c.A.w * co + a.w * cn;
+        c.M = Mn;
+    };
+    // pieces of workgroups wb..we (slot 0 if the workgroup's range starts inside the row at r0,
+    // else slot 1); idx(w, slot) is the piece's index into ml / acc
+    auto fold_range = [&](Acc& c0, Acc& c1, int wb, int we, int64_t r0, const float* ml_b, const float* acc_b,
+                          auto idx, int d0) {
+        const int64_t i_first = idx(wb, r0 <= first_tile(wb) ? 0 : 1);
+        for (int w = wb; w <= we; w += 4) {
+            float2 ml[4];
+            float4 a[4];
+            bool ok[4];
+            int64_t ft[5];
+#pragma unroll
+            for (int k = 0; k < 5; ++k) ft[k] = first_tile(w + k);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int ww = w + k;
+                // (a workgroup whose range is empty — possible when G > U — wrote nothing)
+                ok[k] = ww <= we && ft[k] != ft[k + 1];
+                const int64_t i = ok[k] ? idx(ww, r0 <= ft[k] ? 0 : 1) : i_first;
+                ml[k] = reinterpret_cast<const float2*>(ml_b)[i];
+                a[k] = *reinterpret_cast<const float4*>(acc_b + i * HD + d0);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (ok[k]) fold((k & 1) ? c1 : c0, ml[k], a[k]);
+        }
+    };
+    const int slices = heads_per_row * TPH;
+    for (int sl = static_cast<int>(threadIdx.x); sl < slices; sl += static_cast<int>(blockDim.x)) {
+        const int hh = sl / TPH;
+        const int d0 = (sl % TPH) * 4;
+        Acc c0{kMinusHuge, 0.f, make_float4(0.f, 0.f, 0.f, 0.f)}, c1 = c0;
         const int h = hgi * heads_per_row + hh;      // query head index within the token
         if (member && w0 == w1) {                    // the row's own keys, held whole by one range
-            if (part == 0) {
-                const int64_t idx = (int64_t)t * n_kv * rep + h;
-                fold(reinterpret_cast<const float2*>(mu.ptok_ml)[idx], mu.ptok_acc + idx * HD + d0);
-            }
+            const int64_t i = (int64_t)t * n_kv * rep + h;
+            fold(c0, reinterpret_cast<const float2*>(mu.ptok_ml)[i], *reinterpret_cast<const float4*>(mu.ptok_acc + i * HD + d0));
         } else {
-#pragma unroll 4
-            for (int w = w0 + part; w <= w1; w += 2) {
-                // (a workgroup whose range is empty — possible when G > U — wrote nothing: skip it)
-                if (w * U / G == (w + 1) * U / G) continue;
-                const int slot = (pr0 <= w * U / G) ? 0 : 1;
-                const int64_t idx = (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh;
-                fold(reinterpret_cast<const float2*>(part_ml)[idx], part_acc + idx * HD + d0);
-            }
+            fold_range(c0, c1, w0, w1, pr0, part_ml, part_acc,
+                       [&](int w, int slot) { return (static_cast<int64_t>(w) * 2 + slot) * heads_per_row + hh; }, d0);
         }
         if (member) {                                // the unit's column of this head
             const int wv = hh / rep, col = rep * tu.y + hh % rep;
             if (v0 == v1) {
-                if (part == 0) {
-                    const int64_t idx = (static_cast<int64_t>(tu.x) * wpg + wv) * 16 + col;
-                    fold(reinterpret_cast<const float2*>(mu.punit_ml)[idx], mu.punit_acc + idx * HD + d0);
-                }
+                const int64_t i = (static_cast<int64_t>(tu.x) * wpg + wv) * 16 + col;
+                fold(c0, reinterpret_cast<const float2*>(mu.punit_ml)[i], *reinterpret_cast<const float4*>(mu.punit_acc + i * HD + d0));
             } else {
-                for (int w = v0 + part; w <= v1; w += 2) {
-                    if (w * U / G == (w + 1) * U / G) continue;
-                    const int slot = (q0 <= w * U / G) ? 0 : 1;
-                    const int64_t idx = ((static_cast<int64_t>(w) * 2 + slot) * wpg + wv) * 16 + col;
-                    fold(reinterpret_cast<const float2*>(mu.psh_ml)[idx], mu.psh_acc + idx * HD + d0);
-                }
+                fold_range(c0, c1, v0, v1, q0, mu.psh_ml, mu.psh_acc,
+                           [&](int w, int slot) { return ((static_cast<int64_t>(w) * 2 + slot) * wpg + wv) * 16 + col; }, d0);
             }
         }
-        if (part) {
-            xs[0][ti] = M; xs[1][ti] = L; xs[2][ti] = A.x; xs[3][ti] = A.y; xs[4][ti] = A.z; xs[5][ti] = A.w;
-        }
-        __syncthreads();
-        if (!part) {
-            const float M1 = xs[0][ti], Mn = fmaxf(M, M1);
-            const float c0 = exp2f(M - Mn), c1 = exp2f(M1 - Mn);
-            L = L * c0 + xs[1][ti] * c1;
-            A.x = A.x * c0 + xs[2][ti] * c1;
-            A.y = A.y * c0 + xs[3][ti] * c1;
-            A.z = A.z * c0 + xs[4][ti] * c1;
-            A.w = A.w * c0 + xs[5][ti] * c1;
-            const float f = vfin / L;
-            uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
-            const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
-            const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
-            *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
-        }
-        __syncthreads();                             // xs is reused by the next slice batch
+        const float Mn = fmaxf(c0.M, c1.M);
+        const float e0 = exp2f(c0.M - Mn), e1 = exp2f(c1.M - Mn);
+        const float L = c0.L * e0 + c1.L * e1;
+        float4 A;
+        A.x = c0.A.x * e0 + c1.A.x * e1;
+        A.y = c0.A.y * e0 + c1.A.y * e1;
+        A.z = c0.A.z * e0 + c1.A.z * e1;
+        A.w = c0.A.w * e0 + c1.A.w * e1;
+        const float f = vfin / L;
+        uint16_t* o = out + ((int64_t)t * n_kv * rep + h) * HD + d0;
+        const uint32_t lo = f32_to_bf16_bits(A.x * f) | (uint32_t(f32_to_bf16_bits(A.y * f)) << 16);
+        const uint32_t hi = f32_to_bf16_bits(A.z * f) | (uint32_t(f32_to_bf16_bits(A.w * f)) << 16);
+        *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
     }
 }
 
@@ -1846,8 +1865,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if ((phase & kPhaseMerge) && (G > 1 || units_on)) {
         const dim3 mgrid(static_cast<unsigned>(rows));
         const int nt = static_cast<int>(num_tokens);
-        // two halves of one thread per (head, 4 dims) slice, at most 512 each (more slices loop)
-        const int m2 = 2 * std::min(512, wpg * rep_v * head_dim / 4);
+        // one thread per (head, 4 dims) slice, at most 512 (more slices loop)
+        const int m2 = std::min(512, wpg * rep_v * head_dim / 4);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
