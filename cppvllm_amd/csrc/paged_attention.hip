@@ -1203,12 +1203,19 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             // the first two tiles are in flight before q is staged: their latency covers it (a
             // planned launch issued them at its start when they are the plan's)
             preA = preA && pa_.row == plan_row && ta_ == plan_lt;
-            if (!preA) load_tile(pa_, ta_, A, lookup(pa_, ta_), true);
+            const Phys ph_a = preA ? Phys{0, 0} : lookup(pa_, ta_);
             advance();
             pb_ = lp;
             tb_ = lt;
             preB = preB && preA && pb_.row == pa_.row && tb_ == ta_ + 1;
-            if (!preB) load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
+            // B's loads follow A's on every path through this code (a fresh A always takes a fresh
+            // B), so the compiler's waits for A's registers leave B's loads in flight
+            if (!preA) {
+                load_tile(pa_, ta_, A, ph_a, true);
+                load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
+            } else if (!preB) {
+                load_tile(pb_, tb_, B, lookup(pb_, tb_), pb_.row >= 0);
+            }
             preA = preB = false;
             advance();
             Phys ph = lookup(lp, lt);
@@ -1218,32 +1225,43 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
             reset();
             if constexpr (MF) {
                 // one tile in flight while one is computed (two register tiles): the MFMA tiles
-                // are larger than the VALU ones and three do not fit the register budget
+                // are larger than the VALU ones and three do not fit the register budget. The loop
+                // has a single exit at the bottom (B's loads are issued, as zero-size loads, also
+                // after the last tile): every path back to the loop head then issues A's loads
+                // before B's, so the compiler's wait for a tile leaves the other tile's loads in
+                // flight (an exit from inside the finish makes the compiler's loop flow add paths
+                // without B's loads, and its waits for A then cover B's loads as well).
                 for (;;) {
                     compute(pa_, ta_, A);
                     if (ta_ + 1 == pa_.le) {
                         finish(pa_);
-                        if (pb_.row < 0) break;
-                        reset();
-                        take_q(pb_);
+                        if (pb_.row >= 0) {
+                            reset();
+                            take_q(pb_);
+                        }
                     }
                     pa_ = lp;
                     ta_ = lt;
                     load_tile(pa_, ta_, A, ph, pa_.row >= 0);
                     advance();
                     ph = lookup(lp, lt);
-                    compute(pb_, tb_, B);
-                    if (tb_ + 1 == pb_.le) {
-                        finish(pb_);
-                        if (pa_.row < 0) break;
-                        reset();
-                        take_q(pa_);
+                    const bool live_b = pb_.row >= 0;
+                    if (live_b) {
+                        compute(pb_, tb_, B);
+                        if (tb_ + 1 == pb_.le) {
+                            finish(pb_);
+                            if (pa_.row >= 0) {
+                                reset();
+                                take_q(pa_);
+                            }
+                        }
                     }
                     pb_ = lp;
                     tb_ = lt;
                     load_tile(pb_, tb_, B, ph, pb_.row >= 0);
                     advance();
                     ph = lookup(lp, lt);
+                    if (pa_.row < 0) break;     // the tile after B's: none means B's was the last
                 }
             } else
             for (;;) {
