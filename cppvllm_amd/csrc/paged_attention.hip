@@ -1264,6 +1264,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                     if (pa_.row < 0) break;     // the tile after B's: none means B's was the last
                 }
             } else
+            // the same single bottom exit with three register tiles
             for (;;) {
                 pc_ = lp;
                 tc_ = lt;
@@ -1273,34 +1274,42 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 compute(pa_, ta_, A);
                 if (ta_ + 1 == pa_.le) {
                     finish(pa_);
-                    if (pb_.row < 0) break;
-                    reset();
-                    take_q(pb_);
+                    if (pb_.row >= 0) {
+                        reset();
+                        take_q(pb_);
+                    }
                 }
                 pa_ = lp;
                 ta_ = lt;
                 load_tile(pa_, ta_, A, ph, pa_.row >= 0);
                 advance();
                 ph = lookup(lp, lt);
-                compute(pb_, tb_, B);
-                if (tb_ + 1 == pb_.le) {
-                    finish(pb_);
-                    if (pc_.row < 0) break;
-                    reset();
-                    take_q(pc_);
+                if (pb_.row >= 0) {
+                    compute(pb_, tb_, B);
+                    if (tb_ + 1 == pb_.le) {
+                        finish(pb_);
+                        if (pc_.row >= 0) {
+                            reset();
+                            take_q(pc_);
+                        }
+                    }
                 }
                 pb_ = lp;
                 tb_ = lt;
                 load_tile(pb_, tb_, B, ph, pb_.row >= 0);
                 advance();
                 ph = lookup(lp, lt);
-                compute(pc_, tc_, C);
-                if (tc_ + 1 == pc_.le) {
-                    finish(pc_);
-                    if (pa_.row < 0) break;
-                    reset();
-                    take_q(pa_);
+                if (pc_.row >= 0) {
+                    compute(pc_, tc_, C);
+                    if (tc_ + 1 == pc_.le) {
+                        finish(pc_);
+                        if (pa_.row >= 0) {
+                            reset();
+                            take_q(pa_);
+                        }
+                    }
                 }
+                if (pa_.row < 0) break;         // the tile after C's: none means C's was the last
             }
         }
         rb = rlim;
