@@ -1354,30 +1354,37 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 const int n = ld_uniform(&ur->n, 0);
                 MfTile TA, TB;
                 int tile = pc.lt;
+                // q before the first two tiles (the first compute's wait for q then leaves the tiles
+                // in flight), loaded unconditionally (member 0's row past the unit's members) and
+                // zeroed after: column c = REP j + h is member j's query head REP wi + h
+                uint4 qv[4];
+                const int qj = i16 / REP;
+                {
+                    const int tj = ur->tok[qj < n ? qj : 0];
+                    const uint16_t* src = p.q + ((int64_t)tj * H + REP * wi + i16 % REP) * HD;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st)
+                        qv[st] = *reinterpret_cast<const uint4*>(src + (st >> 1) * 64 + g4 * 16 + (st & 1) * 8);
+                }
                 mf_load(pol, pc, tile, TA, lookup(pc, tile), true);
                 mf_load(pol, pc, min(tile + 1, pc.le - 1), TB, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
-                {   // column c = REP j + h: member j's query head REP wi + h (zero past the unit's members)
-                    const int j = i16 / REP, hh = i16 % REP;
-                    const int tj = j < n ? ur->tok[j] : 0;
-                    const uint16_t* src = p.q + ((int64_t)tj * H + REP * wi + hh) * HD;
 #pragma unroll
-                    for (int st = 0; st < 4; ++st) {
-                        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-                        if (j < n) v = *reinterpret_cast<const uint4*>(src + (st >> 1) * 64 + g4 * 16 + (st & 1) * 8);
-                        qm[st] = __builtin_bit_cast(bf16x8_t, v);
-                    }
-                }
+                for (int st = 0; st < 4; ++st)
+                    qm[st] = __builtin_bit_cast(bf16x8_t, qj < n ? qv[st] : make_uint4(0u, 0u, 0u, 0u));
                 mm = kMinusHuge;
                 lm = 0.f;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) om[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                // single bottom exit (zero-size loads past the piece's end): every path back to the
+                // loop head issues TA's loads before TB's, so each wait leaves the other tile in flight
                 for (;;) {
                     mf_compute(pc, tile, TA);
-                    if (++tile >= pc.le) break;
+                    ++tile;
                     mf_load(pol, pc, min(tile + 1, pc.le - 1), TA, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
-                    mf_compute(pc, tile, TB);
-                    if (++tile >= pc.le) break;
+                    if (tile < pc.le) mf_compute(pc, tile, TB);
+                    ++tile;
                     mf_load(pol, pc, min(tile + 1, pc.le - 1), TB, lookup(pc, min(tile + 1, pc.le - 1)), tile + 1 < pc.le);
+                    if (tile >= pc.le) break;
                 }
                 // partials of all 16 columns: whole units in their own slot, cut ones in the range's
                 const float L = xor32_sum(xor16_sum(lm));
