@@ -28,9 +28,10 @@
 //   * lane = (grp, sub): grp = lane/8 picks one of 8 keys of a step, sub = lane%8 owns a 16-byte
 //     (HD=128) or 8-byte (HD=64) slice of the 128-byte K and V rows, so each load instruction
 //     covers 8 full key rows (8 x 128 B cache lines);
-//   * a tile is 4 steps = 32 keys; the next tile's K/V/scale loads are issued before the current
-//     one is computed (register double buffer, unrolled by two, straight-line prefetch so the wait
-//     before each compute covers only its own tile); block-table lookups run one tile ahead;
+//   * a tile is 4 steps = 32 keys; the next two tiles' K/V/scale loads are in flight while one is
+//     computed (register triple buffer, unrolled by three; the GQA-4/8 MFMA path: two tiles, one in
+//     flight). The tile loops exit only at their bottom and prefetch straight-line, so the wait
+//     before each compute covers only its own tile; block-table lookups run one tile ahead;
 //   * raw buffer loads with the non-temporal hint; a prefetch past the piece's end gets a
 //     zero-size descriptor and returns zeros without memory traffic;
 //   * FP8 -> f32 with the hardware OCP converter (v_cvt_pk_f32_fp8, exact for finite codes);
