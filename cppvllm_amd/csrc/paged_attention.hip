@@ -62,6 +62,10 @@ constexpr float kMinusHuge = -1e30f;
 constexpr int kMaxRows = 8192;             // rows (tokens x head groups) per launch: LDS prefix
 constexpr size_t kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
+// MFMA path: each wave's K tile passes through LDS (32 rows of 128 bytes, rows 144 bytes apart so
+// both the full-row writes and the MFMA-layout reads are bank-conflict free)
+constexpr int kKtRowBytes = 144;
+constexpr int kKtWaveBytes = 32 * kKtRowBytes;
 constexpr int kMaxQRows = 8;
 constexpr int kPreQRows = 4;               // q rows a planned launch fetches ahead of its first tiles
 constexpr int kDeferMinTiles = 16;          // ranges this long hold their first cut piece's partial (MFMA path)
@@ -125,7 +129,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // heads' factors with ds_bpermute. Loads per lane and 32-key tile: 4 x 16 B of K, 8 x 8 B of V and
 // 4 scales (lane r of each row of 16 loads key 4g + r's; the row reads them with DPP broadcasts).
 struct MfTile {
-    uint4 k[2][2];          // [kb][half]: key kb*16 + i16, bytes half*64 + g*16 .. +16 of the head's row
+    uint4 k[2][2];          // [kb][h]: key kb*16 + i16, bytes h*64 + g*16 .. +16 of the head's row
+                            // (with the LDS transpose: [kb][j]: key kb*16 + 8j + lane/8, bytes (lane%8)*16 .. +16)
     uint2 v[2][4];          // [kb][r]: key kb*16 + 4g + r, bytes 8*i16 .. +8
     float ks[2], vs[2];     // [kb]: key kb*16 + 4g + (i16 & 3); lane r of each row of 16 is broadcast
 };
@@ -528,8 +533,9 @@ struct Piece {
 };
 
 // DEFER (MFMA path, full 8-kv-head row groups): the range's first cut piece is stored after the
-// range's tile stream (see `deferred` below); a separate instantiation because the held partial's
-// registers slow the short ranges of the one-kv-head shares down.
+// range's tile stream (see `deferred` below), and K rows are loaded whole and passed through LDS
+// into the MFMA layout (see `mf_load`); a separate instantiation because both slow the short
+// ranges of the one-kv-head shares down.
 template <int HD, int REP, int SM, bool ONE_BLOCK, bool PLANNED, bool SHARED = false, bool DEFER = false>
 __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     using V = KvVec<HD>;
@@ -572,6 +578,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 
     constexpr bool MF = REP >= 4;                   // GQA 4 / 8: score and PV products on MFMA
     constexpr bool DEF = MF && DEFER;
+    constexpr bool KT = DEF;                        // K through the per-wave LDS transpose area
     static_assert(!MF || HD == 128, "the MFMA path is laid out for head_dim 128");
     struct VTile {
         VT k[kSteps], v[kSteps];
@@ -621,10 +628,21 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 const int64_t ph = (ONE_BLOCK || kb == 0) ? ph2.lo : ph2.hi;
                 const auto rk = make_rsrc(p.k_cache + ph * blk_bytes, kv_rec);
                 const auto rv = make_rsrc(p.v_cache + ph * blk_bytes, kv_rec);
-                const uint32_t kin = static_cast<uint32_t>(min(p0 + kb * 16 + i16, pc.kv_len - 1) & bs_mask);
-                const uint32_t koff = kin * row_bytes + col + g4 * 16;
-                tl.k[kb][0] = buf_load<uint4, POL>(rk, koff);
-                tl.k[kb][1] = buf_load<uint4, POL>(rk, koff + 64);
+                if constexpr (KT) {
+                    // K as full 128-byte rows, 8 per load (8 lanes a row): the MFMA layout reads each
+                    // row as two 64-byte halves (~3% slower at GQA 8); mf_compute moves it through LDS
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const uint32_t kin =
+                                static_cast<uint32_t>(min(p0 + kb * 16 + 8 * j + (lane >> 3), pc.kv_len - 1) & bs_mask);
+                        tl.k[kb][j] = buf_load<uint4, POL>(rk, kin * row_bytes + col + (lane & 7) * 16);
+                    }
+                } else {
+                    const uint32_t kin = static_cast<uint32_t>(min(p0 + kb * 16 + i16, pc.kv_len - 1) & bs_mask);
+                    const uint32_t koff = kin * row_bytes + col + g4 * 16;
+                    tl.k[kb][0] = buf_load<uint4, POL>(rk, koff);
+                    tl.k[kb][1] = buf_load<uint4, POL>(rk, koff + 64);
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t vin = static_cast<uint32_t>(min(p0 + kb * 16 + 4 * g4 + r, pc.kv_len - 1) & bs_mask);
@@ -687,6 +705,9 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows_real + p.max_units, p.num_tokens) +
                     static_cast<size_t>(vg) * p.qrows * wpg * QB;
     constexpr int QL = (QB + 1023) / 1024;           // 16-byte loads per lane per row
+    // this wave's K transpose area (MFMA path and units), after the workgroup's q staging
+    char* kt_lds = reinterpret_cast<char*>(prefix) + lds_q_offset(rows_real + p.max_units, p.num_tokens) +
+                   static_cast<size_t>(p.pack) * p.qrows * wpg * QB + static_cast<size_t>(threadIdx.x >> 6) * kKtWaveBytes;
     if constexpr (PLANNED) {
         // Everything the prologue waits for (q of the first rows, prefix, token metadata) is
         // requested before the first two tiles, so the in-order vmcnt wait for it leaves the
@@ -902,6 +923,28 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     };
     auto mf_compute = [&](const Piece& pc, int tile, const MfTile& tl) {
         const int p0 = tile * kTileKeys;
+            // K rows -> LDS (full rows), back in the MFMA layout: key kb*16 + i16, bytes h*64 + g*16 .. +16
+            // (a wave's LDS operations complete in order, so the reads see this tile's writes and
+            // the next tile's writes come after these reads)
+            uint4 kt[2][2];
+            if constexpr (KT) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        *reinterpret_cast<uint4*>(kt_lds + (kb * 16 + 8 * j + (lane >> 3)) * kKtRowBytes + (lane & 7) * 16) =
+                                tl.k[kb][j];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        kt[kb][h] = *reinterpret_cast<const uint4*>(kt_lds + (kb * 16 + i16) * kKtRowBytes + h * 64 + g4 * 16);
+            } else {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) kt[kb][h] = tl.k[kb][h];
+            }
             // S^T for keys kb*16 + 4g + r (rows) x heads (columns)
             float sv[2][4];
 #pragma unroll
@@ -909,7 +952,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
                 f32x4_t sa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
-                    const uint4 kw = tl.k[kb][st >> 1];
+                    const uint4 kw = kt[kb][st >> 1];
                     const bf16x8_t ka = (st & 1) ? fp8x8_bf16(kw.z, kw.w) : fp8x8_bf16(kw.x, kw.y);
                     sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qm[st], sa, 0, 0, 0);
                 }
@@ -1854,9 +1897,13 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
             p.pack = k;
             break;
         }
+    // the per-wave K transpose areas of the full-row-group MFMA launches (launch_decode_p's DEFER
+    // instantiation: GQA 4/8 at head_dim 128, 8 kv heads per workgroup)
+    const size_t kt_area = (rep_v >= 4 && head_dim == 128 && wpg == 8 && p.pack == 1)
+                                   ? static_cast<size_t>(wpg) * kKtWaveBytes : 0;
     {
         // q staging rows: as many as the LDS left by the row prefix and token table allows
-        const size_t fixed = lds_q_offset(static_cast<int>(rows) + p.max_units, static_cast<int>(num_tokens));
+        const size_t fixed = lds_q_offset(static_cast<int>(rows) + p.max_units, static_cast<int>(num_tokens)) + kt_area;
         const size_t per_row = static_cast<size_t>(wpg) * p.pack * rep_v * head_dim * 2;
         const int fit = fixed < kLdsBytes ? static_cast<int>((kLdsBytes - fixed) / per_row) : 0;
         if (fit < 1) return CVH_ERR_UNSUPPORTED;
@@ -1880,7 +1927,7 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if (phase & kPhaseDecode) {
         const int planned = (phase & kPhasePlanned) ? ((phase & kPhaseShared) ? 2 : 1) : 0;
         const size_t lds = lds_q_offset(static_cast<int>(rows) + p.max_units, static_cast<int>(num_tokens)) +
-                           static_cast<size_t>(p.qrows) * wpg * p.pack * rep_v * head_dim * 2;
+                           static_cast<size_t>(p.qrows) * wpg * p.pack * rep_v * head_dim * 2 + kt_area;
         const int WG = G / p.pack, nth = 64 * wpg * p.pack;
         const bool one_block = (1 << lg) >= kTileKeys;
         bool ok;
