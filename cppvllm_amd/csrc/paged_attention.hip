@@ -62,8 +62,8 @@ constexpr float kMinusHuge = -1e30f;
 constexpr int kMaxRows = 8192;             // rows (tokens x head groups) per launch: LDS prefix
 constexpr size_t kLdsBytes = 160 * 1024;   // LDS of one gfx950 workgroup
 constexpr int kQStageBytes = 16384;        // LDS for the q of a workgroup's first rows
-// MFMA path: each wave's K tile passes through LDS (32 rows of 128 bytes, rows 144 bytes apart so
-// both the full-row writes and the MFMA-layout reads are bank-conflict free)
+// Full-row-group MFMA launches: each wave's K tile passes through LDS (32 rows of 128 bytes, rows
+// 144 bytes apart so both the full-row writes and the MFMA-layout reads are bank-conflict free)
 constexpr int kKtRowBytes = 144;
 constexpr int kKtWaveBytes = 32 * kKtRowBytes;
 constexpr int kMaxQRows = 8;
@@ -705,7 +705,7 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
     char* q_lds_b = reinterpret_cast<char*>(prefix) + lds_q_offset(rows_real + p.max_units, p.num_tokens) +
                     static_cast<size_t>(vg) * p.qrows * wpg * QB;
     constexpr int QL = (QB + 1023) / 1024;           // 16-byte loads per lane per row
-    // this wave's K transpose area (MFMA path and units), after the workgroup's q staging
+    // this wave's K transpose area (used by the DEFER instantiation), after the workgroup's q staging
     char* kt_lds = reinterpret_cast<char*>(prefix) + lds_q_offset(rows_real + p.max_units, p.num_tokens) +
                    static_cast<size_t>(p.pack) * p.qrows * wpg * QB + static_cast<size_t>(threadIdx.x >> 6) * kKtWaveBytes;
     if constexpr (PLANNED) {
