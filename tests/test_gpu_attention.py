@@ -134,6 +134,21 @@ def test_max_rows_per_launch(orc):
     assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
 
 
+def test_partition_bounds_past_32_bits(orc):
+    """Tiles x partitions above 2^32: the merge's range bounds take the 64-bit division (32-bit
+    below); the result must match the automatic partition count's and the oracle's sampled rows."""
+    b = synth(41, [1024, 1100, 1500, 2000, 1024, 1300, 1700, 1900], 256, queries_per_seq=1024)
+    U = int(sum((int(k) + 31) // 32 for k in np_(b["token_kv_len"])))
+    G = (1 << 32) // U + 64
+    assert (U + 1) * G > (1 << 32)
+    say(f"partition bounds past 32 bits: U={U} G={G}")
+    db = dev(b)
+    got = run_gpu(db, G)
+    assert_close_bf16(got, run_gpu(db, 0), max_abs=8e-3, mean_abs=5e-4)
+    rows = sorted(np.random.default_rng(47).choice(8192, 96, replace=False).tolist())
+    assert_close_bf16(got[rows], run_oracle(orc, b, rows=rows))
+
+
 @pytest.mark.parametrize("H,HD,limit", [(32, 64, 4096), (64, 64, 2048), (64, 128, 8192)])
 def test_gqa_row_limits(orc, H, HD, limit):
     """At head_dim 64, GQA 4 / 8 run as 2 / 4 virtual kv heads per kv head, so at 8 kv heads a
