@@ -1452,8 +1452,8 @@ __global__ __launch_bounds__(512, 1) void paged_decode_kernel(Params p) {
 // Log-sum-exp merge of cut rows (reference: kernels/paged_attention.cu:361-393). One workgroup
 // per row (token, kv-head group): it recomputes, from the prefix the decode kernel stored, which
 // workgroups covered the row (wave-uniform scalar arithmetic) and exits if one did. One thread
-// per (query head, 4 dims) of the row (wpg * rep * HD / 4 <= 512 for every supported shape:
-// wpg <= 8, rep <= 2 after the virtual-head split, HD <= 128) folds the row's pieces online,
+// per (query head, 4 dims) of the row (wpg * rep * HD / 4 slices: 512 at GQA 2, 2048 at GQA 8,
+// which loop twice over the workgroup's 1024 threads) folds the row's pieces online,
 // w0, w0 + 2, ... into one accumulator and w0 + 1, w0 + 3, ... into another, and combines the two
 // (small batches cut a row into up to 8 pieces; their loads go out four at a time).
 // Shared-prefix inputs of the merge (null when the launch has no units).
@@ -1469,7 +1469,7 @@ struct MergeUnits {
 };
 
 template <int HD, int SM>
-__global__ __launch_bounds__(512) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
+__global__ __launch_bounds__(1024) void paged_merge2_kernel(uint16_t* __restrict__ out, const float* __restrict__ part_acc,
                                                           const float* __restrict__ part_ml,
                                                           const int* __restrict__ prefix,
                                                           const float* __restrict__ v_scale, int num_tokens, int n_kv,
@@ -1947,8 +1947,8 @@ int paged_attention(void* out, const void* q, const uint8_t* k_cache, const uint
     if ((phase & kPhaseMerge) && (G > 1 || units_on)) {
         const dim3 mgrid(static_cast<unsigned>(rows));
         const int nt = static_cast<int>(num_tokens);
-        // one thread per (head, 4 dims) slice, at most 512 (more slices loop)
-        const int m2 = std::min(512, wpg * rep_v * head_dim / 4);
+        // one thread per (head, 4 dims) slice, at most 1024 (GQA 8's 2048 slices loop twice)
+        const int m2 = std::min(1024, wpg * rep_v * head_dim / 4);
         if (head_dim == 128) {
             if (scale_mode == CVH_SCALE_PER_TOKEN_HEAD)
                 paged_merge2_kernel<128, CVH_SCALE_PER_TOKEN_HEAD><<<mgrid, m2, 0, s>>>(
